@@ -1,0 +1,218 @@
+"""Benchmark of the sqrt(N) attention hot path on one MI355X.
+
+Default workload (BASELINE metric): B=1, H=16, D=128, S=131072, fp16, causal,
+q/k/v/dO ~ N(0,1) from an on-device generator (seed 0).  A step is one
+forward + backward of the attention op (o = attn(q, k, v); o.backward(dO)).
+Prints ONE JSON line:
+  value        whole-job effective TFLOP/s of fwd+bwd (14*D*pairs / time)
+  fwd_ms / fwdbwd_ms and their effective TFLOP/s
+  roofline     the forward kernel (one launch of cra_fwd = one kernel), timed
+               with HIP events on the stream it runs on, against the fp16
+               dense MFMA peak; traffic from a committed rocprofv3 --pmc
+               summary when present
+  cpu_baseline the oracle's chunked CPU port on the host cores, on a bounded
+               sample of query rows of the same workload, as TFLOP/s
+
+``--crossover`` instead sweeps S against torch's SDPA (forward and fwd+bwd)
+and prints one JSON line per point.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cron-root-attention_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "fwd & fwd+bwd ms + eff. TFLOP/s, H=16 D=128 S=128K fp16, 1 MI355X"
+PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def pairs_fast(S: int, top_k: int = 2) -> int:
+    import numpy as np
+    W = int(math.ceil(math.sqrt(S)))
+    i = np.arange(S, dtype=np.int64)
+    ls = np.maximum(i - W + 1, 0)
+    p = np.minimum(i + 1, W) + (ls + W - 1) // W
+    if S > 2048:
+        p = p + top_k * (ls // W)
+    return int(p.sum())
+
+
+def row_pairs(rows, S, top_k=2):
+    import numpy as np
+    W = int(math.ceil(math.sqrt(S)))
+    i = np.asarray(rows, dtype=np.int64)
+    ls = np.maximum(i - W + 1, 0)
+    p = np.minimum(i + 1, W) + (ls + W - 1) // W
+    if S > 2048:
+        p = p + top_k * (ls // W)
+    return int(p.sum())
+
+
+def timed(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
+    """Oracle CPU port (fp32) on sampled 256-query chunks, spread evenly over
+    the sequence, until ~budget_s of CPU time; returns TFLOP/s."""
+    import numpy as np
+    import torch
+    from oracle import cra_oracle as O
+    from oracle.cpu_port import cra_cpu_chunked
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    Hs = 2  # heads held in host memory for the sample
+    q = torch.randn(1, Hs, S, D, generator=g)
+    k = torch.randn(1, Hs, S, D, generator=g)
+    v = torch.randn(1, Hs, S, D, generator=g)
+    plan = O.make_plan(S)
+    src = O.relay_select(k, plan, "lanetree")
+    n_chunks = S // 256
+    order = np.random.default_rng(0).permutation(n_chunks)
+    done_rows = []
+    t_used = 0.0
+    for c in order:
+        lo = int(c) * 256
+        t0 = time.perf_counter()
+        cra_cpu_chunked(q, k, v, plan, src=src, q_rows=(lo, lo + 256))
+        t_used += time.perf_counter() - t0
+        done_rows.extend(range(lo, lo + 256))
+        if t_used >= budget_s:
+            break
+    flops = 4 * D * row_pairs(done_rows, S) * Hs
+    return {"value": flops / t_used / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"fp32 forward, {len(done_rows) // 256} random 256-query chunks x {Hs} heads "
+                      f"of S={S}, D={D} ({len(done_rows) * Hs} query rows, {t_used:.1f} s)",
+            "seconds": round(t_used, 2)}
+
+
+def traffic_for(kernel: str, workload: str):
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def run_main(args):
+    import torch
+    import cron_root_attention as cra
+    from cron_root_attention import _native
+    dev = torch.device("cuda", 0)
+    B, H, S, D = 1, 16, 131072, 128
+    dtype = torch.float16
+    gen = torch.Generator(device=dev).manual_seed(0)
+    mk = lambda: torch.randn(B, H, S, D, generator=gen, device=dev, dtype=torch.float32).to(dtype)
+    q, k, v, dO = mk(), mk(), mk(), mk()
+    P = pairs_fast(S)
+    f_fwd = 4 * D * P * B * H
+    f_all = 14 * D * P * B * H
+
+    with torch.no_grad():
+        fwd_ms = timed(lambda: cra.cron_root_attention(q, k, v), args.steps, args.warmup, torch)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        qg.grad = kg.grad = vg.grad = None
+        cra.cron_root_attention(qg, kg, vg).backward(dO)
+
+    step_ms = timed(step, args.steps, args.warmup, torch)
+
+    # forward kernel alone: cra_fwd launches exactly one kernel
+    W = int(math.ceil(math.sqrt(S)))
+    p = _native.problem(B, H, H, S, D, W, True, 2, dtype, 1 / math.sqrt(D))
+    gk, gv, _ = _native.build_global(p, k, v, None)
+    kern_ms = timed(lambda: _native.forward(p, q, k, v, gk, gv), args.steps, args.warmup, torch)
+    achieved = f_fwd / (kern_ms * 1e-3) / 1e12
+    workload = "H16_D128_S131072_fp16"
+    roof = {"kernel": "fwd_kernel<f16,128>", "bound": "mfma", "achieved": round(achieved, 2),
+            "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic_for("fwd", workload), "avg_ms": round(kern_ms, 4),
+            "algorithmic_flops": f_fwd}
+
+    cpu = None
+    if not args.skip_cpu:
+        cpu = cpu_baseline(B, H, S, D, args.cpu_seconds, args.cpu_threads)
+
+    out = {
+        "metric": METRIC, "value": round(f_all / (step_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic: q, k, v, dO ~ N(0,1), on-device generator seed 0",
+        "config": {"workload": "fwd+bwd of sqrt(N) attention, B=1 H=16 D=128 S=131072 fp16 "
+                               "causal (BASELINE config 3 at the north-star S)",
+                   "B": B, "H": H, "S": S, "D": D, "window": W, "relay_top_k": 2},
+        "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 3),
+        "fwdbwd_ms": round(step_ms, 4), "fwdbwd_tflops": round(f_all / (step_ms * 1e-3) / 1e12, 3),
+        "pairs_per_head": P, "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def run_crossover(args):
+    import torch
+    import torch.nn.functional as F
+    import cron_root_attention as cra
+    dev = torch.device("cuda", 0)
+    for (B, H, D, dtype) in ((2, 32, 128, torch.bfloat16), (1, 16, 128, torch.float16),
+                             (1, 8, 64, torch.float16)):
+        for S in (256, 512, 768, 1024, 1536, 2048, 3072, 4096, 8192, 16384):
+            g = torch.Generator(device=dev).manual_seed(0)
+            q, k, v, do = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=dtype)
+                           for _ in range(4))
+            res = {"B": B, "H": H, "D": D, "S": S, "dtype": str(dtype).split(".")[-1]}
+            for name, fn in (("cra", lambda a, b, c: cra.cron_root_attention(a, b, c)),
+                             ("sdpa", lambda a, b, c: F.scaled_dot_product_attention(
+                                 a, b, c, is_causal=True))):
+                with torch.no_grad():
+                    res[f"{name}_fwd_ms"] = round(timed(lambda: fn(q, k, v), 20, 5, torch), 4)
+                qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+                def st():
+                    qg.grad = kg.grad = vg.grad = None
+                    fn(qg, kg, vg).backward(do)
+                res[f"{name}_train_ms"] = round(timed(st, 10, 3, torch), 4)
+            print(json.dumps(res), flush=True)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--crossover", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "sharding across GPUs is design-only", file=sys.stderr)
+        return 2
+    if args.crossover:
+        run_crossover(args)
+    else:
+        run_main(args)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,74 @@
+"""sqrt(N) sparse causal attention for MI355X (gfx950), drop-in for the
+reference package's public API (reference __init__.py:206-222).
+
+    from cron_root_attention import cron_root_attention, CronRootAttention
+    o = cron_root_attention(q, k, v)          # q, k, v: [B, H, S, D] on a ROCm GPU
+
+All compute runs in the hand-written HIP library ``libcra_hip.so`` next to
+this file (build: ``python cron-root-attention_amd/build.py``).
+"""
+
+__version__ = "0.1.0"
+
+import torch as _torch
+
+from .core import (GPU_SM_MAP, CronRootAttentionV14, CronRootAttentionV14Function,
+                   cron_root_attention_v14, cron_root_attention_varlen, get_num_sms,
+                   warmup_varlen_shapes)
+from .hybrid import CronRootAttentionHybrid, cron_root_attention_hybrid
+from .module import CronRootAttention, CronRootMultiheadAttention
+from . import _native
+
+
+def calibrate(H: int = 8, D: int = 64, dtype=None, S: int = 4096, verbose: bool = True) -> dict:
+    """Warm the kernels once for (H, D) (reference __init__.py:84-180).
+
+    The reference benchmarks Triton (num_warps, num_stages) candidates here.
+    The HIP kernels have one compiled tile configuration per (dtype, D), so
+    this runs one forward+backward at S and reports that configuration.
+    """
+    dtype = dtype or _torch.float16
+    dev = _torch.device("cuda", _torch.cuda.current_device())
+    q = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
+    k = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
+    v = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
+    cron_root_attention_v14(q, k, v).sum().backward()
+    _torch.cuda.synchronize(dev)
+    cfg = {"fwd": ("wave64x4", "q128"), "bwd": ("wave64x4", "k128")}
+    if verbose:
+        print(f"  H={H} D={D}: fwd={cfg['fwd']} bwd={cfg['bwd']} (static gfx950 tiles)")
+    return cfg
+
+
+def get_gpu_info() -> dict:
+    """Device name and CU count (reference __init__.py:183-202)."""
+    if not _torch.cuda.is_available():
+        return {"gpu_name": "No GPU", "sm_count": 0, "is_known_gpu": False}
+    name = _torch.cuda.get_device_name()
+    info = {"gpu_name": name, "sm_count": get_num_sms(),
+            "is_known_gpu": name in GPU_SM_MAP or any(n in name for n in GPU_SM_MAP)}
+    try:
+        d = _native.device_info(_torch.cuda.current_device())
+        info.update({"arch": d["arch"], "lds_bytes_per_cu": d["lds_bytes_per_cu"]})
+    except Exception:  # library not built: report torch's view only
+        pass
+    return info
+
+
+cron_root_attention = cron_root_attention_v14
+
+__all__ = [
+    "cron_root_attention",
+    "cron_root_attention_v14",
+    "cron_root_attention_varlen",
+    "warmup_varlen_shapes",
+    "CronRootAttention",
+    "CronRootMultiheadAttention",
+    "cron_root_attention_hybrid",
+    "CronRootAttentionHybrid",
+    "calibrate",
+    "get_num_sms",
+    "get_gpu_info",
+    "GPU_SM_MAP",
+    "__version__",
+]

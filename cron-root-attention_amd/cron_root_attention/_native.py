@@ -1,0 +1,224 @@
+"""ctypes binding of libcra_hip.so (the C ABI declared in include/cra.h).
+
+PyTorch supplies device memory and the current HIP stream; every buffer is
+allocated here with torch and passed to the library as a raw pointer plus
+element strides.  The library itself allocates nothing and never
+synchronises.
+
+If the library is missing or cannot be loaded every entry point raises
+:class:`CraLibraryError`: there is no fallback computation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+_LIB_NAME = "libcra_hip.so"
+_lock = threading.Lock()
+_lib = None
+_lib_error: Optional[str] = None
+
+F16, BF16, F32 = 0, 1, 2
+_DTYPE_CODE = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+# return codes (include/cra.h)
+OK, E_INVALID, E_LAYOUT, E_DTYPE, E_UNSUPPORTED, E_HIP, E_WORKSPACE = 0, -1, -2, -3, -4, -5, -6
+
+
+class CraError(RuntimeError):
+    """A libcra_hip call returned an error code."""
+
+    def __init__(self, code: int, func: str, message: str):
+        self.code = code
+        super().__init__(f"{func}: {message} (code {code})")
+
+
+class CraLibraryError(RuntimeError):
+    """libcra_hip.so is missing or cannot be loaded."""
+
+
+class CraProblem(ctypes.Structure):
+    _fields_ = [
+        ("B", ctypes.c_int32), ("H_q", ctypes.c_int32), ("H_kv", ctypes.c_int32),
+        ("S", ctypes.c_int32), ("D", ctypes.c_int32), ("W", ctypes.c_int32),
+        ("relay", ctypes.c_int32), ("top_k", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+class CraTensor(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("sb", ctypes.c_int64), ("sh", ctypes.c_int64),
+                ("ss", ctypes.c_int64)]
+
+
+class CraDeviceInfo(ctypes.Structure):
+    _fields_ = [("cu_count", ctypes.c_int32), ("lds_bytes_per_cu", ctypes.c_int32),
+                ("arch_major", ctypes.c_int32), ("arch_minor", ctypes.c_int32),
+                ("arch_name", ctypes.c_char * 64), ("device_name", ctypes.c_char * 128)]
+
+
+# Exported symbols and their signatures (mirrors include/cra.h).
+_P = ctypes.POINTER(CraProblem)
+_SIGNATURES = {
+    "cra_supported_head_dim": (ctypes.c_int, [ctypes.c_int32]),
+    "cra_global_rows": (ctypes.c_int64, [_P]),
+    "cra_build_global": (ctypes.c_int, [_P, CraTensor, CraTensor, ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "cra_fwd": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
+                               ctypes.c_void_p, CraTensor, ctypes.c_void_p, ctypes.c_void_p]),
+    "cra_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
+    "cra_bwd": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, CraTensor, CraTensor,
+                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                               ctypes.c_void_p, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
+                               ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "cra_device_info": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(CraDeviceInfo)]),
+    "cra_strerror": (ctypes.c_char_p, [ctypes.c_int32]),
+    "cra_last_error": (ctypes.c_char_p, []),
+    "cra_abi_version": (ctypes.c_int32, []),
+}
+ABI_VERSION = 1
+
+
+def library_path() -> str:
+    return os.environ.get("CRA_HIP_LIBRARY",
+                          os.path.join(os.path.dirname(os.path.abspath(__file__)), _LIB_NAME))
+
+
+def load_library():
+    """Load (once) and return the ctypes handle; raise CraLibraryError if absent."""
+    global _lib, _lib_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not os.path.exists(path):
+            raise CraLibraryError(
+                f"{path} not found: build it with `python cron-root-attention_amd/build.py` "
+                "(this package has no non-HIP fallback)")
+        try:
+            lib = ctypes.CDLL(path)
+        except OSError as e:
+            raise CraLibraryError(f"cannot load {path}: {e}") from e
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.cra_abi_version() != ABI_VERSION:
+            raise CraLibraryError(f"{path}: ABI {lib.cra_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def _raise(code: int, func: str):
+    lib = load_library()
+    msg = (lib.cra_last_error() or b"").decode() or lib.cra_strerror(code).decode()
+    if code in (E_INVALID, E_LAYOUT):
+        raise ValueError(f"{func}: {msg}")
+    if code == E_DTYPE:
+        raise TypeError(f"{func}: {msg}")
+    if code == E_UNSUPPORTED:
+        raise NotImplementedError(f"{func}: {msg}")
+    raise CraError(code, func, msg)
+
+
+def _check(code: int, func: str):
+    if code != OK:
+        _raise(code, func)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; use float16, bfloat16 or float32") from None
+
+
+def problem(B, H_q, H_kv, S, D, W, relay, top_k, dtype, scale) -> CraProblem:
+    return CraProblem(B, H_q, H_kv, S, D, W, 1 if relay else 0, top_k if relay else 0,
+                      dtype_code(dtype), float(scale))
+
+
+def tensor_arg(t: torch.Tensor) -> CraTensor:
+    assert t.dim() == 4 and t.stride(3) == 1
+    return CraTensor(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def supported_head_dim(D: int) -> bool:
+    return bool(load_library().cra_supported_head_dim(D))
+
+
+def global_rows(p: CraProblem) -> int:
+    n = load_library().cra_global_rows(ctypes.byref(p))
+    if n < 0:
+        _raise(E_INVALID, "cra_global_rows")
+    return int(n)
+
+
+def build_global(p: CraProblem, k: torch.Tensor, v: torch.Tensor,
+                 relay_scale: Optional[torch.Tensor]):
+    """Packed strided+relay rows (glob_k, glob_v) and relay source rows."""
+    lib = load_library()
+    G = global_rows(p)
+    B, Hkv, D = p.B, p.H_kv, p.D
+    gk = torch.empty(B, Hkv, G, D, dtype=k.dtype, device=k.device)
+    gv = torch.empty_like(gk)
+    nb = (p.S + p.W - 1) // p.W
+    src = (torch.empty(B, Hkv, nb * p.top_k, dtype=torch.int32, device=k.device)
+           if p.relay else None)
+    rs = relay_scale.data_ptr() if (relay_scale is not None and p.relay) else None
+    _check(lib.cra_build_global(ctypes.byref(p), tensor_arg(k), tensor_arg(v), gk.data_ptr(),
+                                gv.data_ptr(), src.data_ptr() if src is not None else None, rs,
+                                _stream(k)), "cra_build_global")
+    return gk, gv, src
+
+
+def forward(p: CraProblem, q, k, v, gk, gv):
+    lib = load_library()
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(p.B, p.H_q, p.S, dtype=torch.float32, device=q.device)
+    _check(lib.cra_fwd(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                       gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(), _stream(q)),
+           "cra_fwd")
+    return o, lse
+
+
+def workspace_bytes(p: CraProblem) -> int:
+    return int(load_library().cra_bwd_workspace_bytes(ctypes.byref(p)))
+
+
+def backward(p: CraProblem, q, k, v, o, do, lse, gk, gv, src, relay_scale, want_dalpha: bool):
+    lib = load_library()
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    nbytes = workspace_bytes(p)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    dalpha = (torch.empty(p.H_kv, dtype=torch.float32, device=q.device)
+              if (want_dalpha and p.relay) else None)
+    rs = relay_scale.data_ptr() if (relay_scale is not None and p.relay) else None
+    _check(lib.cra_bwd(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                       tensor_arg(o), tensor_arg(do), lse.data_ptr(), gk.data_ptr(),
+                       gv.data_ptr(), src.data_ptr() if src is not None else None, rs,
+                       tensor_arg(dq), tensor_arg(dk), tensor_arg(dv),
+                       dalpha.data_ptr() if dalpha is not None else None, ws.data_ptr(),
+                       ws.numel(), _stream(q)), "cra_bwd")
+    return dq, dk, dv, dalpha
+
+
+def device_info(index: int = 0) -> dict:
+    lib = load_library()
+    info = CraDeviceInfo()
+    _check(lib.cra_device_info(index, ctypes.byref(info)), "cra_device_info")
+    return {"cu_count": info.cu_count, "lds_bytes_per_cu": info.lds_bytes_per_cu,
+            "arch": info.arch_name.decode(), "name": info.device_name.decode(),
+            "arch_major": info.arch_major, "arch_minor": info.arch_minor}

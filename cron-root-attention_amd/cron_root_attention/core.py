@@ -1,0 +1,273 @@
+"""Entry points and autograd of the sqrt(N) sparse attention on MI355X.
+
+Drop-in for the reference's ``core.py`` surface: ``cron_root_attention_v14``
+(core.py:3767-3797), ``CronRootAttentionV14Function`` (core.py:2822-3759),
+``cron_root_attention_varlen`` / ``warmup_varlen_shapes`` (core.py:3836-4022),
+``get_num_sms`` / ``GPU_SM_MAP`` (core.py:58-188).
+
+Planning follows the reference: W = ceil(sqrt(S)) (core.py:3479), relay only
+for S > 2048 (core.py:2832, 3507), relay_top_k rows per block (core.py:3771),
+logit scale 1/sqrt(D) (core.py:954).  The compute runs in libcra_hip.so:
+``cra_build_global`` packs the strided and top-k relay rows, ``cra_fwd`` runs
+the three phases, ``cra_bwd`` produces dQ/dK/dV (and the relay-scale
+gradient).  Unlike the reference:
+
+* CPU tensors raise instead of running a CPU implementation (the reference
+  dispatches them to ``cra_cpu_fast_compiled``, core.py:3794-3796);
+* the backward returns fresh tensors (the reference returns static CUDA-graph
+  buffers, core.py:3016-3020, 3367-3369) and runs on the caller's current
+  stream (the reference replays on the default stream, core.py:3011);
+* gradients accumulate in fp32 and round once, deterministically (the
+  reference adds fp16 atomics, core.py:1886-1889);
+* with ``relay_log_scale`` the gradient reaching the relay source rows
+  carries the exp(alpha) factor (the reference's scatter drops it,
+  core.py:3541-3544 vs 3274-3290);
+* ``use_persistent`` is accepted and has no numerical effect, as in the
+  reference, whose persistent kernel computes the same no-relay function
+  (core.py:711-900): this build has one forward kernel for all S.
+"""
+from __future__ import annotations
+
+import math
+from functools import lru_cache
+from typing import Optional, Sequence, Union
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _native
+
+RELAY_THRESHOLD = 2048          # core.py:2832
+_SUPPORTED_D = (32, 64, 128)
+
+# CU counts for the persistent-grid helpers (reference GPU_SM_MAP, core.py:58-135,
+# lists NVIDIA parts only).
+GPU_SM_MAP = {
+    "AMD Instinct MI355X": 256,
+    "AMD Instinct MI350X": 256,
+    "AMD Instinct MI325X": 304,
+    "AMD Instinct MI300X": 304,
+    "AMD Instinct MI300A": 228,
+    "AMD Instinct MI250X": 220,
+    "AMD Instinct MI210": 104,
+}
+
+
+@lru_cache(maxsize=None)
+def _num_sms_for(device_index: int) -> int:
+    props = torch.cuda.get_device_properties(device_index)
+    n = getattr(props, "multi_processor_count", 0)
+    if n > 0:
+        return n
+    name = torch.cuda.get_device_name(device_index)
+    for known, cu in GPU_SM_MAP.items():
+        if known in name or name in known:
+            return cu
+    return 256
+
+
+def get_num_sms() -> int:
+    """Compute units of the current device (reference core.py:137-170)."""
+    if not torch.cuda.is_available():
+        return 1
+    return _num_sms_for(torch.cuda.current_device())
+
+
+def window_size(S: int) -> int:
+    """W = ceil(sqrt(S)) (core.py:3479)."""
+    return int(math.ceil(math.sqrt(S)))
+
+
+def _padded_head_dim(D: int) -> int:
+    for d in _SUPPORTED_D:
+        if D <= d:
+            return d
+    raise NotImplementedError(f"head dim {D} > 128 is not built for gfx950 in this release")
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """d contiguous, 16-byte aligned rows; otherwise a contiguous copy."""
+    vec = 16 // t.element_size()
+    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0
+          and all(s % vec == 0 for s in t.stride()[:3]))
+    return t if ok else t.contiguous()
+
+
+def _pad_d(t: torch.Tensor, Dp: int) -> torch.Tensor:
+    D = t.shape[-1]
+    return t if D == Dp else F.pad(t, (0, Dp - D))
+
+
+def _check_inputs(q, k, v, kv_groups):
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [B, H, S, D]")
+    B, Hq, S, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError(f"k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    Hkv = k.shape[1]
+    if kv_groups < 1 or Hkv * kv_groups != Hq:
+        raise ValueError(f"H_q={Hq} must equal H_kv={Hkv} * kv_groups={kv_groups}")
+    if S < 1 or B < 1 or D < 1:
+        raise ValueError("B, S and D must be >= 1")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"unsupported dtype {q.dtype}; use float16, bfloat16 or float32")
+    if q.device.type != "cuda":
+        raise RuntimeError(
+            "cron_root_attention runs on ROCm GPU tensors only in this build "
+            f"(got device {q.device}); move q, k, v to a HIP device")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, v must be on the same device")
+
+
+class CronRootAttentionV14Function(torch.autograd.Function):
+    """Autograd of the three-phase attention (reference core.py:2822-3759).
+
+    ``apply(q, k, v, use_persistent, kv_groups, relay_log_scale, relay_top_k)``
+    as in the reference; two trailing optional arguments override the window
+    and the relay switch (used by tests to run the CPU-path semantics of
+    ``cra_cpu_fast``: floor window, relay always on).
+    """
+
+    RELAY_THRESHOLD = RELAY_THRESHOLD
+    FUSED_BWD_THRESHOLD = 8192  # inert in the reference too (core.py:2836, 3656)
+
+    @staticmethod
+    def forward(ctx, q, k, v, use_persistent: bool = False, kv_groups: int = 1,
+                relay_log_scale: Optional[torch.Tensor] = None, relay_top_k: int = 2,
+                window: Optional[int] = None, relay: Optional[bool] = None):
+        _check_inputs(q, k, v, kv_groups)
+        B, Hq, S, D = q.shape
+        Hkv = k.shape[1]
+        W = window_size(S) if window is None else int(window)
+        relay_on = (S > RELAY_THRESHOLD) if relay is None else bool(relay)
+        if relay_on and not 1 <= relay_top_k <= 4:
+            raise ValueError(f"relay_top_k={relay_top_k} outside [1, 4]")
+        Dp = _padded_head_dim(D)
+        qp, kp, vp = (_kernel_ready(_pad_d(t, Dp)) for t in (q, k, v))
+        p = _native.problem(B, Hq, Hkv, S, Dp, W, relay_on, relay_top_k, q.dtype,
+                            1.0 / math.sqrt(D))
+        rscale = None
+        if relay_log_scale is not None and relay_on:
+            if relay_log_scale.shape != (Hkv,):
+                raise ValueError(f"relay_log_scale must have shape [{Hkv}]")
+            # exp(alpha) rounded to the input dtype, as core.py:3542
+            rscale = relay_log_scale.detach().exp().to(q.dtype).to(torch.float32).contiguous()
+        gk, gv, src = _native.build_global(p, kp, vp, rscale)
+        o, lse = _native.forward(p, qp, kp, vp, gk, gv)
+        ctx.problem = p
+        ctx.D = D
+        ctx.has_alpha = relay_log_scale is not None and relay_on
+        ctx.alpha_dtype = relay_log_scale.dtype if relay_log_scale is not None else None
+        ctx.save_for_backward(qp, kp, vp, o, lse, gk, gv, src, rscale)
+        return o if Dp == D else o[..., :D].contiguous()
+
+    @staticmethod
+    def backward(ctx, do):
+        qp, kp, vp, o, lse, gk, gv, src, rscale = ctx.saved_tensors
+        p = ctx.problem
+        D = ctx.D
+        dop = _kernel_ready(_pad_d(do.to(qp.dtype), p.D))
+        dq, dk, dv, dalpha = _native.backward(p, qp, kp, vp, o, dop, lse, gk, gv, src, rscale,
+                                              ctx.has_alpha)
+        if p.D != D:
+            dq, dk, dv = (t[..., :D].contiguous() for t in (dq, dk, dv))
+        da = dalpha.to(ctx.alpha_dtype) if (ctx.has_alpha and dalpha is not None) else None
+        return dq, dk, dv, None, None, da, None, None, None
+
+
+@torch.compiler.disable
+def cron_root_attention_v14(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                            use_persistent: bool = False, kv_groups: int = 1,
+                            relay_log_scale: Optional[torch.Tensor] = None,
+                            relay_top_k: int = 2) -> torch.Tensor:
+    """sqrt(N) sparse causal attention (reference core.py:3767-3797).
+
+    Args:
+        q: [B, H_q, S, D]; k, v: [B, H_kv, S, D] with H_q = H_kv * kv_groups.
+        use_persistent: accepted for compatibility; no numerical effect.
+        kv_groups: query heads per kv head (query head h reads kv head
+            h // kv_groups, core.py:981).
+        relay_log_scale: optional [H_kv]; relay rows are scaled by
+            exp(relay_log_scale) (core.py:3541-3544); differentiable.
+        relay_top_k: relay rows per sqrt(N) block (1..4).
+
+    Returns: [B, H_q, S, D] in the dtype of q.
+    """
+    return CronRootAttentionV14Function.apply(q, k, v, use_persistent, kv_groups,
+                                              relay_log_scale, relay_top_k)
+
+
+def _attention_with_plan(q, k, v, window: int, relay: bool, kv_groups: int = 1,
+                         relay_log_scale=None, relay_top_k: int = 2):
+    """Same op with an explicit window and relay switch (test hook)."""
+    return CronRootAttentionV14Function.apply(q, k, v, False, kv_groups, relay_log_scale,
+                                              relay_top_k, window, relay)
+
+
+@torch.compiler.disable
+def cron_root_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                               cu_seqlens: Union[Sequence[int], torch.Tensor],
+                               kv_groups: int = 1, use_persistent: bool = False,
+                               relay_log_scale: Optional[torch.Tensor] = None,
+                               relay_top_k: int = 2) -> torch.Tensor:
+    """Packed documents, no attention across boundaries (reference core.py:3836-3954).
+
+    ``cu_seqlens`` (list or CPU tensor, length n_docs + 1, from 0 to S_total)
+    splits the sequence axis; each document is attended on its own with the
+    window and relay rule of its own length.  Documents are zero-copy views
+    (``narrow``); the per-document results are written into one output.
+    """
+    if isinstance(cu_seqlens, torch.Tensor):
+        if cu_seqlens.device.type != "cpu":
+            raise ValueError("cu_seqlens must be a CPU tensor (or list); call .cpu() first")
+        seqs = [int(x) for x in cu_seqlens.tolist()]
+    else:
+        seqs = [int(x) for x in cu_seqlens]
+    S_total = q.shape[2]
+    if len(seqs) < 2 or seqs[0] != 0 or seqs[-1] != S_total or any(
+            b <= a for a, b in zip(seqs, seqs[1:])):
+        raise ValueError(f"cu_seqlens must rise strictly from 0 to {S_total}, got {seqs}")
+    if len(seqs) == 2:
+        return cron_root_attention_v14(q, k, v, use_persistent, kv_groups, relay_log_scale,
+                                       relay_top_k)
+    parts = []
+    for s, e in zip(seqs, seqs[1:]):
+        parts.append(cron_root_attention_v14(q.narrow(2, s, e - s), k.narrow(2, s, e - s),
+                                             v.narrow(2, s, e - s), use_persistent, kv_groups,
+                                             relay_log_scale, relay_top_k))
+    return torch.cat(parts, dim=2)
+
+
+def warmup_varlen_shapes(doc_lengths, H: int, D: int, B: int = 1, kv_groups: int = 1,
+                         dtype=None, device=None, verbose: bool = False) -> None:
+    """Run forward+backward once per distinct length (reference core.py:3957-4022).
+
+    The HIP library has no JIT or graph capture to warm, so this only
+    touches the caching allocator for each shape; kept for API compatibility.
+    """
+    dtype = dtype or torch.float16
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    Hkv = H // kv_groups
+    for S in sorted({int(x) for x in doc_lengths if int(x) > 0}):
+        q = torch.randn(B, H, S, D, device=device, dtype=dtype, requires_grad=True)
+        k = torch.randn(B, Hkv, S, D, device=device, dtype=dtype, requires_grad=True)
+        v = torch.randn(B, Hkv, S, D, device=device, dtype=dtype, requires_grad=True)
+        cron_root_attention_v14(q, k, v, kv_groups=kv_groups).sum().backward()
+        if verbose:
+            print(f"[warmup_varlen_shapes] S={S} done")
+    torch.cuda.synchronize(device)
+
+
+class CronRootAttentionV14(nn.Module):
+    """Module wrapper of the functional op (reference core.py:4025-4051)."""
+
+    def __init__(self, use_persistent: bool = False, auto_persistent_threshold: int = 0):
+        super().__init__()
+        self.use_persistent = use_persistent
+        self.auto_persistent_threshold = auto_persistent_threshold
+
+    def forward(self, q, k, v):
+        return cron_root_attention_v14(q, k, v, use_persistent=self.use_persistent)

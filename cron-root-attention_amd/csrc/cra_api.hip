@@ -1,0 +1,242 @@
+// C-ABI front end of libcra_hip.so: argument validation, planning of the
+// launch geometry and error reporting. Declarations and the contract live in
+// include/cra.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/cra.h"
+#include "cra_common.hpp"
+#include "cra_internal.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(CRA_E_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+int elem_size(int dtype) { return dtype == CRA_F32 ? 4 : 2; }
+
+int check_problem(const cra_problem* p) {
+  if (!p) return fail(CRA_E_INVALID, "problem is NULL");
+  if (p->dtype != CRA_F16 && p->dtype != CRA_BF16 && p->dtype != CRA_F32)
+    return fail(CRA_E_DTYPE, "unknown dtype code %d", p->dtype);
+  if (p->B < 1 || p->H_q < 1 || p->H_kv < 1 || p->S < 1)
+    return fail(CRA_E_INVALID, "B, H_q, H_kv, S must be >= 1 (got %d, %d, %d, %d)", p->B, p->H_q,
+                p->H_kv, p->S);
+  if (p->H_q % p->H_kv)
+    return fail(CRA_E_INVALID, "H_q (%d) must be a multiple of H_kv (%d)", p->H_q, p->H_kv);
+  if (!cra_supported_head_dim(p->D))
+    return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128)", p->D);
+  if (p->W < 1 || p->W > p->S)
+    return fail(CRA_E_INVALID, "window W=%d outside [1, S=%d]", p->W, p->S);
+  if (p->relay != 0 && p->relay != 1) return fail(CRA_E_INVALID, "relay must be 0 or 1");
+  if (p->relay && (p->top_k < 1 || p->top_k > 4))
+    return fail(CRA_E_INVALID, "top_k=%d outside [1, 4]", p->top_k);
+  if (!(p->scale > 0.f)) return fail(CRA_E_INVALID, "scale must be > 0");
+  // 32-bit row indices inside the kernels
+  if ((int64_t)p->B * p->H_q * (int64_t)p->S > (int64_t)1 << 31)
+    return fail(CRA_E_INVALID, "B*H*S exceeds 2^31");
+  return CRA_OK;
+}
+
+int check_tensor(const char* name, const cra_tensor& t, int esz) {
+  if (!t.ptr) return fail(CRA_E_INVALID, "%s: NULL pointer", name);
+  if (reinterpret_cast<uintptr_t>(t.ptr) % 16)
+    return fail(CRA_E_LAYOUT, "%s: pointer not 16-byte aligned", name);
+  const int64_t vec = 16 / esz;
+  if (t.sb % vec || t.sh % vec || t.ss % vec)
+    return fail(CRA_E_LAYOUT, "%s: strides (%lld, %lld, %lld) must be multiples of %lld elements",
+                name, (long long)t.sb, (long long)t.sh, (long long)t.ss, (long long)vec);
+  return CRA_OK;
+}
+
+int check_buf(const char* name, const void* p) {
+  if (!p) return fail(CRA_E_INVALID, "%s: NULL pointer", name);
+  if (reinterpret_cast<uintptr_t>(p) % 16)
+    return fail(CRA_E_LAYOUT, "%s: pointer not 16-byte aligned", name);
+  return CRA_OK;
+}
+
+int64_t num_blocks(const cra_problem* p) { return (p->S + p->W - 1) / p->W; }
+int rows_per_block(const cra_problem* p) { return p->relay ? 1 + p->top_k : 1; }
+
+}  // namespace
+
+extern "C" {
+
+int cra_supported_head_dim(int32_t D) { return D == 32 || D == 64 || D == 128; }
+
+int32_t cra_abi_version(void) { return CRA_ABI_VERSION; }
+
+int64_t cra_global_rows(const cra_problem* p) {
+  if (check_problem(p)) return -1;
+  return num_blocks(p) * rows_per_block(p);
+}
+
+int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glob_k, void* glob_v,
+                     int32_t* relay_src, const float* relay_scale, void* stream) {
+  if (int e = check_problem(p)) return e;
+  const int esz = elem_size(p->dtype);
+  if (int e = check_tensor("k", k, esz)) return e;
+  if (int e = check_tensor("v", v, esz)) return e;
+  if (int e = check_buf("glob_k", glob_k)) return e;
+  if (int e = check_buf("glob_v", glob_v)) return e;
+  if (p->relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
+  cra::GlobalArgs a{};
+  a.k = k.ptr;
+  a.v = v.ptr;
+  a.ksb = k.sb; a.ksh = k.sh; a.kss = k.ss;
+  a.vsb = v.sb; a.vsh = v.sh; a.vss = v.ss;
+  a.gk = glob_k;
+  a.gv = glob_v;
+  a.src = relay_src;
+  a.scale = relay_scale;
+  a.Hkv = p->H_kv;
+  a.S = p->S;
+  a.W = p->W;
+  a.NB = (int)num_blocks(p);
+  a.rpb = rows_per_block(p);
+  a.top_k = p->relay ? p->top_k : 0;
+  a.relay = p->relay;
+  a.G = num_blocks(p) * a.rpb;
+  if ((int64_t)p->B * p->H_kv > 65535) return fail(CRA_E_INVALID, "B*H_kv exceeds 65535");
+  hipError_t e = cra::launch_build_global(p->dtype, p->D, a, p->B, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "cra_build_global launch");
+  return CRA_OK;
+}
+
+int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, const void* glob_k,
+            const void* glob_v, cra_tensor o, float* lse, void* stream) {
+  if (int e = check_problem(p)) return e;
+  const int esz = elem_size(p->dtype);
+  if (int e = check_tensor("q", q, esz)) return e;
+  if (int e = check_tensor("k", k, esz)) return e;
+  if (int e = check_tensor("v", v, esz)) return e;
+  if (int e = check_tensor("o", o, esz)) return e;
+  if (int e = check_buf("glob_k", glob_k)) return e;
+  if (int e = check_buf("glob_v", glob_v)) return e;
+  if (int e = check_buf("lse", lse)) return e;
+  cra::FwdArgs a{};
+  a.q = q.ptr; a.k = k.ptr; a.v = v.ptr; a.gk = glob_k; a.gv = glob_v; a.o = o.ptr; a.lse = lse;
+  a.qsb = q.sb; a.qsh = q.sh; a.qss = q.ss;
+  a.ksb = k.sb; a.ksh = k.sh; a.kss = k.ss;
+  a.vsb = v.sb; a.vsh = v.sh; a.vss = v.ss;
+  a.osb = o.sb; a.osh = o.sh; a.oss = o.ss;
+  a.B = p->B; a.Hq = p->H_q; a.Hkv = p->H_kv; a.S = p->S; a.W = p->W;
+  a.rpb = rows_per_block(p);
+  a.G = num_blocks(p) * a.rpb;
+  a.scale = p->scale;
+  a.ntiles = (p->S + 127) / 128;
+  hipError_t e = cra::launch_fwd(p->dtype, p->D, a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "cra_fwd launch");
+  return CRA_OK;
+}
+
+size_t cra_bwd_workspace_bytes(const cra_problem* p) {
+  if (check_problem(p)) return 0;
+  int nchunk = 0, chunk_len = 0;
+  return cra::bwd_workspace_bytes(p->D, p->B, p->H_q, p->H_kv, p->S, p->W,
+                                  num_blocks(p) * rows_per_block(p), &nchunk, &chunk_len);
+}
+
+int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+            cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
+            const int32_t* relay_src, const float* relay_scale, cra_tensor dq, cra_tensor dk,
+            cra_tensor dv, float* dalpha, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int e = check_problem(p)) return e;
+  const int esz = elem_size(p->dtype);
+  if (int e = check_tensor("q", q, esz)) return e;
+  if (int e = check_tensor("k", k, esz)) return e;
+  if (int e = check_tensor("v", v, esz)) return e;
+  if (int e = check_tensor("o", o, esz)) return e;
+  if (int e = check_tensor("dout", dout, esz)) return e;
+  if (int e = check_tensor("dq", dq, esz)) return e;
+  if (int e = check_tensor("dk", dk, esz)) return e;
+  if (int e = check_tensor("dv", dv, esz)) return e;
+  if (int e = check_buf("lse", lse)) return e;
+  if (int e = check_buf("glob_k", glob_k)) return e;
+  if (int e = check_buf("glob_v", glob_v)) return e;
+  if (p->relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
+  const int64_t G = num_blocks(p) * rows_per_block(p);
+  int nchunk = 0, chunk_len = 0;
+  const size_t need = cra::bwd_workspace_bytes(p->D, p->B, p->H_q, p->H_kv, p->S, p->W, G,
+                                               &nchunk, &chunk_len);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(CRA_E_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
+                workspace ? workspace_bytes : (size_t)0);
+  if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(CRA_E_LAYOUT, "workspace not 256-byte aligned");
+  cra::BwdArgs a{};
+  a.q = q.ptr; a.k = k.ptr; a.v = v.ptr; a.o = o.ptr; a.dout = dout.ptr; a.lse = lse;
+  a.gk = glob_k; a.gv = glob_v; a.src = relay_src; a.rscale = relay_scale;
+  a.dq = dq.ptr; a.dk = dk.ptr; a.dv = dv.ptr;
+  a.qsb = q.sb; a.qsh = q.sh; a.qss = q.ss;
+  a.ksb = k.sb; a.ksh = k.sh; a.kss = k.ss;
+  a.vsb = v.sb; a.vsh = v.sh; a.vss = v.ss;
+  a.osb = o.sb; a.osh = o.sh; a.oss = o.ss;
+  a.dosb = dout.sb; a.dosh = dout.sh; a.doss = dout.ss;
+  a.dqsb = dq.sb; a.dqsh = dq.sh; a.dqss = dq.ss;
+  a.dksb = dk.sb; a.dksh = dk.sh; a.dkss = dk.ss;
+  a.dvsb = dv.sb; a.dvsh = dv.sh; a.dvss = dv.ss;
+  a.B = p->B; a.Hq = p->H_q; a.Hkv = p->H_kv; a.S = p->S; a.W = p->W;
+  a.rpb = rows_per_block(p);
+  a.top_k = p->relay ? p->top_k : 0;
+  a.relay = p->relay;
+  a.G = G;
+  a.scale = p->scale;
+  a.nchunk = nchunk;
+  a.chunk_len = chunk_len;
+  // workspace carve-up: delta [B*Hq*S] fp32, then the global-row partials
+  char* ws = static_cast<char*>(workspace);
+  const size_t delta_bytes = (((size_t)p->B * p->H_q * p->S * 4) + 255) / 256 * 256;
+  a.delta = reinterpret_cast<float*>(ws);
+  a.gpart = reinterpret_cast<float*>(ws + delta_bytes);
+  a.dalpha = dalpha;
+  hipError_t e = cra::launch_bwd(p->dtype, p->D, a, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "cra_bwd launch");
+  return CRA_OK;
+}
+
+int cra_device_info(int32_t device, cra_device_info_t* out) {
+  if (!out) return fail(CRA_E_INVALID, "out is NULL");
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  memset(out, 0, sizeof(*out));
+  out->cu_count = prop.multiProcessorCount;
+  out->lds_bytes_per_cu = (int32_t)prop.maxSharedMemoryPerMultiProcessor;
+  out->arch_major = prop.major;
+  out->arch_minor = prop.minor;
+  snprintf(out->arch_name, sizeof(out->arch_name), "%s", prop.gcnArchName);
+  snprintf(out->device_name, sizeof(out->device_name), "%s", prop.name);
+  return CRA_OK;
+}
+
+const char* cra_strerror(int32_t code) {
+  switch (code) {
+    case CRA_OK: return "ok";
+    case CRA_E_INVALID: return "invalid argument";
+    case CRA_E_LAYOUT: return "unsupported layout";
+    case CRA_E_DTYPE: return "unknown dtype";
+    case CRA_E_UNSUPPORTED: return "unsupported configuration";
+    case CRA_E_HIP: return "HIP runtime error";
+    case CRA_E_WORKSPACE: return "workspace too small";
+  }
+  return "unknown error";
+}
+
+const char* cra_last_error(void) { return g_err; }
+
+}  // extern "C"

@@ -1,0 +1,633 @@
+// Backward of the three-phase sqrt(N) attention.
+//
+// Reference: `CronRootAttentionV14Function.backward` (core.py:3626-3759) runs
+// dQ (core.py:1165-1316), local dK/dV (core.py:1650-1745), strided dK/dV with
+// fp16 atomics (core.py:1755-1889), relay dK/dV (core.py:2381-2492) and a
+// read-add-store scatter of the relay gradients onto their source rows
+// (core.py:2767-2815). Math per pair (i, j): P = exp(s - LSE_i),
+// dP = dO_i . v_j, dS = P (dP - Delta_i), Delta_i = O_i . dO_i;
+// dQ_i += scale dS k_j, dK_j += scale dS q_i, dV_j += P dO_i.
+//
+// This build keeps every accumulation in fp32 and rounds once:
+//   1. delta_kernel      Delta = rowsum(O * dO)                       (fp32)
+//   2. dq_kernel         query-centric: local band + global prefix -> dQ
+//   3. dkdv_kernel<GLOB> packed global rows (strided + relay), query range
+//                        split in chunks -> fp32 partials in the workspace
+//   4. dalpha_kernel     (optional) gradient of the relay log-scale
+//   5. dkdv_kernel<LOC>  key-centric local band; its epilogue adds the
+//                        chunk partials of the global rows whose source is
+//                        the key row (strided row r*W, relay source rows) and
+//                        writes dK/dV once.
+// No atomics: every output row has exactly one writer and the partial sums
+// are reduced in a fixed order, so two runs give identical bits.
+#include "cra_common.hpp"
+#include "cra_internal.hpp"
+
+namespace cra {
+
+namespace {
+
+template <typename T, int D>
+struct BwdTraits {
+  static constexpr int kThreads = 256;
+  static constexpr int kQW = 32;                        // dq: queries per wave
+  static constexpr int kBM = 128;                       // dq: queries per workgroup
+  static constexpr int kBN = sizeof(T) == 4 ? 32 : 64;  // dq: key rows per tile
+  static constexpr int kKW = 32;                        // dkdv: key rows per wave
+  static constexpr int kBK = 128;                       // dkdv: key rows per workgroup
+  static constexpr int kBQ = sizeof(T) == 4 ? 32 : 64;  // dkdv: queries per tile
+  static constexpr int kDC = D / 32;
+  static constexpr int kDB = D / 16;
+  static constexpr int kLD = D + 16 / (int)sizeof(T);
+  static constexpr int kLDTN = kBN + 4;
+  static constexpr int kLDTQ = kBQ + 4;
+};
+
+template <typename T>
+__device__ __forceinline__ void zero_frag(Frag<T>& f) {
+#pragma unroll
+  for (int w = 0; w < Frag<T>::kWords; ++w) f.w[w] = make_uint4(0, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const f32x4& v, float mul) {
+  T e[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) e[r] = from_f32<T>(v[r] * mul);
+  if constexpr (sizeof(T) == 2)
+    *reinterpret_cast<uint2*>(p) = *reinterpret_cast<const uint2*>(e);
+  else
+    *reinterpret_cast<uint4*>(p) = *reinterpret_cast<const uint4*>(e);
+}
+
+// First query that sees packed global row gr (inverse of glob_prefix).
+__device__ __forceinline__ int glob_row_first_query(int gr, int W, int rpb) {
+  const int r = gr / rpb;
+  return (gr - r * rpb) == 0 ? r * W + W : (r + 1) * W + W - 1;
+}
+
+// ---------------------------------------------------------------------------
+// 1. Delta = rowsum(O * dO)
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void delta_kernel(BwdArgs a) {
+  constexpr int kLPR = D / 8;
+  constexpr int kRows = 256 / kLPR;
+  const int bh = blockIdx.y;
+  const int b = bh / a.Hq, h = bh % a.Hq;
+  const int tid = threadIdx.x;
+  const int li = tid % kLPR;
+  const int row = blockIdx.x * kRows + tid / kLPR;
+  float acc = 0.f;
+  if (row < a.S) {
+    const Frag<T> o = lds_frag_row<T>(static_cast<const T*>(a.o) + b * a.osb + h * a.osh +
+                                      (int64_t)row * a.oss + li * 8);
+    const Frag<T> d = lds_frag_row<T>(static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh +
+                                      (int64_t)row * a.doss + li * 8);
+    const T* eo = reinterpret_cast<const T*>(o.w);
+    const T* ed = reinterpret_cast<const T*>(d.w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += to_f32(eo[i]) * to_f32(ed[i]);
+  }
+#pragma unroll
+  for (int off = kLPR / 2; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+  if (row < a.S && li == 0) a.delta[(int64_t)bh * a.S + row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// 2. dQ, query-centric (mirror of the forward's tiling)
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool MASK, typename Valid>
+__device__ __forceinline__ void dq_tile(const T* sK, const T* sV, const T* sKt,
+                                        const Frag<T> (&qf)[2][BwdTraits<T, D>::kDC],
+                                        const Frag<T> (&df)[2][BwdTraits<T, D>::kDC],
+                                        f32x4 (&dqa)[BwdTraits<T, D>::kDB][2],
+                                        const float (&lse2)[2], const float (&dl)[2], float c2,
+                                        int l16, int g, Valid valid) {
+  using Tr = BwdTraits<T, D>;
+  constexpr int kKB = Tr::kBN / 16, kKC = Tr::kBN / 32;
+  Frag<T> dsf[kKC][2];
+  float ds[kKB][2][4];
+#pragma unroll
+  for (int kb = 0; kb < kKB; ++kb) {
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, p0 = s0, p1 = s0;
+#pragma unroll
+    for (int c = 0; c < Tr::kDC; ++c) {
+      const Frag<T> kf = lds_frag_row<T>(sK + (16 * kb + l16) * Tr::kLD + 32 * c + 8 * g);
+      const Frag<T> vf = lds_frag_row<T>(sV + (16 * kb + l16) * Tr::kLD + 32 * c + 8 * g);
+      s0 = mma(s0, kf, qf[0][c]);
+      s1 = mma(s1, kf, qf[1][c]);
+      p0 = mma(p0, vf, df[0][c]);
+      p1 = mma(p1, vf, df[1][c]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ko = 16 * kb + 4 * g + r;
+      float x0 = s0[r] * c2 - lse2[0];
+      float x1 = s1[r] * c2 - lse2[1];
+      if (MASK) {
+        if (!valid(ko, 0)) x0 = -__builtin_huge_valf();
+        if (!valid(ko, 1)) x1 = -__builtin_huge_valf();
+      }
+      ds[kb][0][r] = __builtin_amdgcn_exp2f(x0) * (p0[r] - dl[0]);
+      ds[kb][1][r] = __builtin_amdgcn_exp2f(x1) * (p1[r] - dl[1]);
+    }
+  }
+#pragma unroll
+  for (int kc = 0; kc < kKC; ++kc) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float v8[8] = {ds[2 * kc][qb][0],     ds[2 * kc][qb][1],     ds[2 * kc][qb][2],
+                           ds[2 * kc][qb][3],     ds[2 * kc + 1][qb][0], ds[2 * kc + 1][qb][1],
+                           ds[2 * kc + 1][qb][2], ds[2 * kc + 1][qb][3]};
+      dsf[kc][qb] = pack8<T>(v8);
+    }
+  }
+#pragma unroll
+  for (int db = 0; db < Tr::kDB; ++db) {
+    const T* row = sKt + (16 * db + l16) * Tr::kLDTN;
+#pragma unroll
+    for (int kc = 0; kc < kKC; ++kc) {
+      const Frag<T> kt = lds_frag_2x4<T>(row + 32 * kc + 4 * g, row + 32 * kc + 16 + 4 * g);
+      dqa[db][0] = mma(dqa[db][0], kt, dsf[kc][0]);
+      dqa[db][1] = mma(dqa[db][1], kt, dsf[kc][1]);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dq_kernel(BwdArgs a, int ntiles) {
+  using Tr = BwdTraits<T, D>;
+  __shared__ __attribute__((aligned(16))) T sK[Tr::kBN * Tr::kLD];
+  __shared__ __attribute__((aligned(16))) T sV[Tr::kBN * Tr::kLD];
+  __shared__ __attribute__((aligned(16))) T sKt[D * Tr::kLDTN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nbh = a.B * a.Hq;
+  const int bh = blockIdx.x % nbh;
+  const int tile = ntiles - 1 - (int)(blockIdx.x / nbh);
+  const int b = bh / a.Hq, h = bh % a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int m0 = tile * Tr::kBM;
+  const int q0 = m0 + wave * Tr::kQW;
+  const int S = a.S, W = a.W;
+
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+  const T* dop = static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* gkp = static_cast<const T*>(a.gk) + gbase;
+  const T* gvp = static_cast<const T*>(a.gv) + gbase;
+
+  Frag<T> qf[2][Tr::kDC], df[2][Tr::kDC];
+  int qi[2];
+  float lse2[2], dl[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    qi[qb] = q0 + 16 * qb + l16;
+    const bool ok = qi[qb] < S;
+    lse2[qb] = ok ? a.lse[(int64_t)bh * S + qi[qb]] * kLog2e : 0.f;
+    dl[qb] = ok ? a.delta[(int64_t)bh * S + qi[qb]] : 0.f;
+#pragma unroll
+    for (int c = 0; c < Tr::kDC; ++c) {
+      if (ok) {
+        qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qi[qb] * a.qss + 32 * c + 8 * g);
+        df[qb][c] = lds_frag_row<T>(dop + (int64_t)qi[qb] * a.doss + 32 * c + 8 * g);
+      } else {
+        zero_frag(qf[qb][c]);
+        zero_frag(df[qb][c]);
+      }
+    }
+  }
+  const float c2 = a.scale * kLog2e;
+  f32x4 dqa[Tr::kDB][2];
+#pragma unroll
+  for (int db = 0; db < Tr::kDB; ++db) dqa[db][0] = dqa[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool active = q0 < S;
+  const int q_last = min(q0 + Tr::kQW, S) - 1;
+  TileStage<T, D, Tr::kBN, Tr::kThreads> stk, stv;
+
+  const int lo = max(0, m0 - W + 1);
+  const int hi = min(S, m0 + Tr::kBM);
+  const int w_lo = max(0, q0 - W + 1);
+  for (int ts = lo; ts < hi; ts += Tr::kBN) {
+    stk.load(kp, a.kss, ts, 0, hi, tid);
+    stv.load(vp, a.vss, ts, 0, hi, tid);
+    __syncthreads();
+    stk.template store_rows<Tr::kLD>(sK, tid);
+    stk.template store_cols<Tr::kLDTN>(sKt, tid);
+    stv.template store_rows<Tr::kLD>(sV, tid);
+    __syncthreads();
+    if (active && ts <= q_last && ts + Tr::kBN - 1 >= w_lo) {
+      const bool full = ts >= q_last - W + 1 && ts + Tr::kBN - 1 <= q0;
+      auto valid = [&](int ko, int qb) {
+        const int j = ts + ko;
+        return j <= qi[qb] && j >= qi[qb] - W + 1;
+      };
+      if (full)
+        dq_tile<T, D, false>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+      else
+        dq_tile<T, D, true>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+    }
+  }
+
+  const int gmax = glob_prefix(hi - 1, W, a.rpb);
+  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+  for (int ts = 0; ts < gmax; ts += Tr::kBN) {
+    stk.load(gkp, D, ts, 0, gmax, tid);
+    stv.load(gvp, D, ts, 0, gmax, tid);
+    __syncthreads();
+    stk.template store_rows<Tr::kLD>(sK, tid);
+    stk.template store_cols<Tr::kLDTN>(sKt, tid);
+    stv.template store_rows<Tr::kLD>(sV, tid);
+    __syncthreads();
+    if (active && ts < wg_hi) {
+      auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
+      if (ts + Tr::kBN <= wg_lo)
+        dq_tile<T, D, false>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+      else
+        dq_tile<T, D, true>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+    }
+  }
+
+  T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    if (!active || qi[qb] >= S) continue;
+    T* row = dqp + (int64_t)qi[qb] * a.dqss;
+#pragma unroll
+    for (int db = 0; db < Tr::kDB; ++db) store4<T>(row + 16 * db + 4 * g, dqa[db][qb], a.scale);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3/5. dK, dV, key-centric. GLOB: the keys are packed global rows and the
+// result is an fp32 partial per query chunk; LOC: the keys are rows of k/v,
+// the queries their local band, and the epilogue folds in the global rows.
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool GLOB, bool MASK>
+__device__ __forceinline__ void dkdv_tile(const T* sQ, const T* sO, const T* sQt, const T* sOt,
+                                          const float* sL, const float* sDl, const int* sGl,
+                                          const Frag<T> (&kf)[2][BwdTraits<T, D>::kDC],
+                                          const Frag<T> (&vf)[2][BwdTraits<T, D>::kDC],
+                                          f32x4 (&dka)[BwdTraits<T, D>::kDB][2],
+                                          f32x4 (&dva)[BwdTraits<T, D>::kDB][2], float c2,
+                                          int l16, int g, int ts, int kw, int W, int q_hi) {
+  using Tr = BwdTraits<T, D>;
+  constexpr int kQS = Tr::kBQ / 32;  // 32-query steps per tile
+#pragma unroll
+  for (int qs = 0; qs < kQS; ++qs) {
+    float p[2][2][4], ds[2][2][4];  // [query block][key block][r]
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int qo = 32 * qs + 16 * qb;
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, d0 = s0, d1 = s0;
+#pragma unroll
+      for (int c = 0; c < Tr::kDC; ++c) {
+        const Frag<T> qa = lds_frag_row<T>(sQ + (qo + l16) * Tr::kLD + 32 * c + 8 * g);
+        const Frag<T> oa = lds_frag_row<T>(sO + (qo + l16) * Tr::kLD + 32 * c + 8 * g);
+        s0 = mma(s0, qa, kf[0][c]);
+        s1 = mma(s1, qa, kf[1][c]);
+        d0 = mma(d0, oa, vf[0][c]);
+        d1 = mma(d1, oa, vf[1][c]);
+      }
+      const f32x4 lq = *reinterpret_cast<const f32x4*>(sL + qo + 4 * g);
+      const f32x4 dq = *reinterpret_cast<const f32x4*>(sDl + qo + 4 * g);
+      int gq[4] = {0, 0, 0, 0};
+      if (GLOB && MASK) {
+        const int4 t4 = *reinterpret_cast<const int4*>(sGl + qo + 4 * g);
+        gq[0] = t4.x; gq[1] = t4.y; gq[2] = t4.z; gq[3] = t4.w;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qabs = ts + qo + 4 * g + r;
+        float x0 = s0[r] * c2 - lq[r];
+        float x1 = s1[r] * c2 - lq[r];
+        if (MASK) {
+          const int j0 = kw + l16, j1 = kw + 16 + l16;
+          bool v0, v1;
+          if (GLOB) {
+            v0 = qabs < q_hi && j0 < gq[r];
+            v1 = qabs < q_hi && j1 < gq[r];
+          } else {
+            v0 = qabs < q_hi && j0 <= qabs && j0 >= qabs - W + 1;
+            v1 = qabs < q_hi && j1 <= qabs && j1 >= qabs - W + 1;
+          }
+          if (!v0) x0 = -__builtin_huge_valf();
+          if (!v1) x1 = -__builtin_huge_valf();
+        }
+        p[qb][0][r] = __builtin_amdgcn_exp2f(x0);
+        p[qb][1][r] = __builtin_amdgcn_exp2f(x1);
+        ds[qb][0][r] = p[qb][0][r] * (d0[r] - dq[r]);
+        ds[qb][1][r] = p[qb][1][r] * (d1[r] - dq[r]);
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const float pv[8] = {p[0][kb][0], p[0][kb][1], p[0][kb][2], p[0][kb][3],
+                           p[1][kb][0], p[1][kb][1], p[1][kb][2], p[1][kb][3]};
+      const float dv8[8] = {ds[0][kb][0], ds[0][kb][1], ds[0][kb][2], ds[0][kb][3],
+                            ds[1][kb][0], ds[1][kb][1], ds[1][kb][2], ds[1][kb][3]};
+      const Frag<T> pf = pack8<T>(pv);
+      const Frag<T> sf = pack8<T>(dv8);
+#pragma unroll
+      for (int db = 0; db < Tr::kDB; ++db) {
+        const T* orow = sOt + (16 * db + l16) * Tr::kLDTQ + 32 * qs;
+        const T* qrow = sQt + (16 * db + l16) * Tr::kLDTQ + 32 * qs;
+        const Frag<T> ot = lds_frag_2x4<T>(orow + 4 * g, orow + 16 + 4 * g);
+        const Frag<T> qt = lds_frag_2x4<T>(qrow + 4 * g, qrow + 16 + 4 * g);
+        dva[db][kb] = mma(dva[db][kb], ot, pf);
+        dka[db][kb] = mma(dka[db][kb], qt, sf);
+      }
+    }
+  }
+}
+
+template <typename T, int D, bool GLOB>
+__global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
+  using Tr = BwdTraits<T, D>;
+  __shared__ __attribute__((aligned(16))) T sQ[Tr::kBQ * Tr::kLD];
+  __shared__ __attribute__((aligned(16))) T sO[Tr::kBQ * Tr::kLD];
+  __shared__ __attribute__((aligned(16))) T sQt[D * Tr::kLDTQ];
+  __shared__ __attribute__((aligned(16))) T sOt[D * Tr::kLDTQ];
+  __shared__ __attribute__((aligned(16))) float sL[Tr::kBQ];
+  __shared__ __attribute__((aligned(16))) float sDl[Tr::kBQ];
+  __shared__ __attribute__((aligned(16))) int sGl[Tr::kBQ];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nbh = a.B * a.Hkv;
+  const int bhk = blockIdx.x % nbh;
+  const int rest = blockIdx.x / nbh;
+  const int chunk = GLOB ? rest % a.nchunk : 0;
+  const int tile = GLOB ? rest / a.nchunk : rest;
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int grp = a.Hq / a.Hkv;
+  const int S = a.S, W = a.W;
+  const int nrows = GLOB ? (int)a.G : S;
+  const int k0 = tile * Tr::kBK;
+  const int kw = k0 + wave * Tr::kKW;
+
+  const T* kbase;
+  const T* vbase;
+  int64_t kstride, vstride;
+  if (GLOB) {
+    const int64_t gb = (int64_t)bhk * a.G * D;
+    kbase = static_cast<const T*>(a.gk) + gb;
+    vbase = static_cast<const T*>(a.gv) + gb;
+    kstride = D;
+    vstride = D;
+  } else {
+    kbase = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+    vbase = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+    kstride = a.kss;
+    vstride = a.vss;
+  }
+
+  // K^T, V^T as B operands: lane holds row kw + 16kb + l16, dims 32c + 8g ..
+  Frag<T> kf[2][Tr::kDC], vf[2][Tr::kDC];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int row = kw + 16 * kb + l16;
+#pragma unroll
+    for (int c = 0; c < Tr::kDC; ++c) {
+      if (row < nrows) {
+        kf[kb][c] = lds_frag_row<T>(kbase + (int64_t)row * kstride + 32 * c + 8 * g);
+        vf[kb][c] = lds_frag_row<T>(vbase + (int64_t)row * vstride + 32 * c + 8 * g);
+      } else {
+        zero_frag(kf[kb][c]);
+        zero_frag(vf[kb][c]);
+      }
+    }
+  }
+  f32x4 dka[Tr::kDB][2], dva[Tr::kDB][2];
+#pragma unroll
+  for (int db = 0; db < Tr::kDB; ++db)
+    dka[db][0] = dka[db][1] = dva[db][0] = dva[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Query range of the workgroup and of this wave.
+  const bool active = kw < nrows;
+  int q_lo, q_hi, wq_lo, wq_hi;
+  if (GLOB) {
+    const int c_lo = chunk * a.chunk_len;
+    const int c_hi = min(S, c_lo + a.chunk_len);
+    q_lo = max(c_lo, glob_row_first_query(k0, W, a.rpb));
+    q_hi = c_hi;
+    wq_lo = active ? max(c_lo, glob_row_first_query(kw, W, a.rpb)) : S;
+    wq_hi = c_hi;
+  } else {
+    q_lo = k0;
+    q_hi = min(S, k0 + Tr::kBK - 1 + W);
+    wq_lo = kw;
+    wq_hi = min(S, kw + Tr::kKW - 1 + W);
+  }
+  const int k_last = min(kw + Tr::kKW, nrows) - 1;
+  const float c2 = a.scale * kLog2e;
+  TileStage<T, D, Tr::kBQ, Tr::kThreads> stq, sto;
+
+  for (int j = 0; j < grp; ++j) {
+    const int h = hk * grp + j;
+    const int bh = b * a.Hq + h;
+    const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+    const T* dop = static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh;
+    for (int ts = q_lo; ts < q_hi; ts += Tr::kBQ) {
+      stq.load(qp, a.qss, ts, 0, q_hi, tid);
+      sto.load(dop, a.doss, ts, 0, q_hi, tid);
+      __syncthreads();
+      stq.template store_rows<Tr::kLD>(sQ, tid);
+      stq.template store_cols<Tr::kLDTQ>(sQt, tid);
+      sto.template store_rows<Tr::kLD>(sO, tid);
+      sto.template store_cols<Tr::kLDTQ>(sOt, tid);
+      if (tid < Tr::kBQ) {
+        const int qabs = ts + tid;
+        const bool ok = qabs < q_hi;
+        sL[tid] = ok ? a.lse[(int64_t)bh * S + qabs] * kLog2e : 0.f;
+        sDl[tid] = ok ? a.delta[(int64_t)bh * S + qabs] : 0.f;
+        if (GLOB) sGl[tid] = ok ? glob_prefix(qabs, W, a.rpb) : 0;
+      }
+      __syncthreads();
+      const int t_last = min(ts + Tr::kBQ, q_hi) - 1;
+      if (active && t_last >= wq_lo && ts < wq_hi) {
+        bool full;
+        if (GLOB)
+          full = ts + Tr::kBQ <= q_hi && glob_prefix(ts, W, a.rpb) > k_last;
+        else
+          full = ts >= k_last && ts + Tr::kBQ - 1 - W + 1 <= kw && ts + Tr::kBQ <= q_hi;
+        if (full)
+          dkdv_tile<T, D, GLOB, false>(sQ, sO, sQt, sOt, sL, sDl, sGl, kf, vf, dka, dva, c2, l16,
+                                       g, ts, kw, W, q_hi);
+        else
+          dkdv_tile<T, D, GLOB, true>(sQ, sO, sQt, sOt, sL, sDl, sGl, kf, vf, dka, dva, c2, l16,
+                                      g, ts, kw, W, q_hi);
+      }
+    }
+  }
+
+  // Epilogue. Lane owns key row kw + 16kb + l16, dims 16db + 4g .. +4.
+  if (GLOB) {
+    float* part = a.gpart + ((int64_t)chunk * nbh + bhk) * a.G * 2 * D;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int row = kw + 16 * kb + l16;
+      if (row >= nrows) continue;
+      float* pk = part + (int64_t)row * 2 * D;
+#pragma unroll
+      for (int db = 0; db < Tr::kDB; ++db) {
+        *reinterpret_cast<f32x4*>(pk + 16 * db + 4 * g) = dka[db][kb] * a.scale;
+        *reinterpret_cast<f32x4*>(pk + D + 16 * db + 4 * g) = dva[db][kb];
+      }
+    }
+    return;
+  }
+  T* dkp = static_cast<T*>(a.dk) + b * a.dksb + hk * a.dksh;
+  T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh;
+  const float rsc = (a.relay && a.rscale) ? a.rscale[hk] : 1.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int j = kw + 16 * kb + l16;
+    if (j >= S) continue;
+#pragma unroll
+    for (int db = 0; db < Tr::kDB; ++db) dka[db][kb] *= a.scale;
+    // Global rows whose source is row j: the strided row of its block and
+    // any relay row selected from it (reference scatter, core.py:2767-2815).
+    const int rblk = j / W;
+    int grow[5];
+    float gsc[5];
+    int nm = 0;
+    if (j == rblk * W) {
+      grow[nm] = rblk * a.rpb;
+      gsc[nm++] = 1.f;
+    }
+    if (a.relay) {
+      const int32_t* src = a.src + ((int64_t)bhk * (a.G / a.rpb) + rblk) * a.top_k;
+      for (int t = 0; t < a.top_k; ++t) {
+        if (src[t] == j) {
+          grow[nm] = rblk * a.rpb + 1 + t;
+          gsc[nm++] = rsc;
+        }
+      }
+    }
+    for (int m = 0; m < nm; ++m) {
+      for (int c = 0; c < a.nchunk; ++c) {
+        const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + grow[m]) * 2 * D;
+#pragma unroll
+        for (int db = 0; db < Tr::kDB; ++db) {
+          dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
+          dva[db][kb] += *reinterpret_cast<const f32x4*>(pk + D + 16 * db + 4 * g) * gsc[m];
+        }
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < Tr::kDB; ++db) {
+      store4<T>(dkp + (int64_t)j * a.dkss + 16 * db + 4 * g, dka[db][kb], 1.f);
+      store4<T>(dvp + (int64_t)j * a.dvss + 16 * db + 4 * g, dva[db][kb], 1.f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. d(relay_log_scale)[hk] = sum over b and relay rows of dRK.RK + dRV.RV
+// (reference core.py:3363-3366), one workgroup per kv head, fixed order.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dalpha_kernel(BwdArgs a) {
+  const int hk = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nbh = a.B * a.Hkv;
+  const int nrel = (int)(a.G / a.rpb) * a.top_k;
+  float acc = 0.f;
+  for (int b = 0; b < a.B; ++b) {
+    const int bhk = b * a.Hkv + hk;
+    const T* gk = static_cast<const T*>(a.gk) + (int64_t)bhk * a.G * D;
+    const T* gv = static_cast<const T*>(a.gv) + (int64_t)bhk * a.G * D;
+    for (int e = tid; e < nrel * D; e += 256) {
+      const int t = e / D, d = e % D;
+      const int row = (t / a.top_k) * a.rpb + 1 + t % a.top_k;
+      float dk = 0.f, dv = 0.f;
+      for (int c = 0; c < a.nchunk; ++c) {
+        const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + row) * 2 * D;
+        dk += pk[d];
+        dv += pk[D + d];
+      }
+      acc += dk * to_f32(gk[(int64_t)row * D + d]) + dv * to_f32(gv[(int64_t)row * D + d]);
+    }
+  }
+  __shared__ float red[256];
+  red[tid] = acc;
+  __syncthreads();
+  for (int off = 128; off >= 1; off >>= 1) {
+    if (tid < off) red[tid] += red[tid + off];
+    __syncthreads();
+  }
+  if (tid == 0) a.dalpha[hk] = red[0];
+}
+
+template <typename T, int D>
+hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
+  using Tr = BwdTraits<T, D>;
+  constexpr int kRows = 256 / (D / 8);
+  hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq), dim3(256),
+                     0, st, a);
+  const int qtiles = (a.S + Tr::kBM - 1) / Tr::kBM;
+  hipLaunchKernelGGL((dq_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
+  const int gtiles = (int)((a.G + Tr::kBK - 1) / Tr::kBK);
+  hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv), dim3(256),
+                     0, st, a, gtiles);
+  if (a.dalpha && a.relay)
+    hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
+  const int ktiles = (a.S + Tr::kBK - 1) / Tr::kBK;
+  hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st, a,
+                     ktiles);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
+  switch (D) {
+    case 32: return launch_TD<T, 32>(a, st);
+    case 64: return launch_TD<T, 64>(a, st);
+    case 128: return launch_TD<T, 128>(a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int W, int64_t G, int* nchunk,
+                           int* chunk_len) {
+  (void)W;
+  // Enough global-row workgroups to cover the chip twice: tiles of 128 rows
+  // per (b, kv head), query range cut into chunks (multiples of 64 queries).
+  const int64_t gtiles = (G + 127) / 128;
+  const int64_t base = gtiles * B * Hkv;
+  int64_t nc = (1024 + base - 1) / base;
+  const int64_t max_nc = (S + 255) / 256;
+  if (nc > max_nc) nc = max_nc;
+  if (nc < 1) nc = 1;
+  int64_t len = (S + nc - 1) / nc;
+  len = (len + 63) / 64 * 64;
+  nc = (S + len - 1) / len;
+  *nchunk = (int)nc;
+  *chunk_len = (int)len;
+  const size_t delta = (((size_t)B * Hq * S * 4) + 255) / 256 * 256;
+  const size_t part = (size_t)nc * B * Hkv * G * 2 * D * 4;
+  return delta + part;
+}
+
+hipError_t launch_bwd(int dtype, int D, const BwdArgs& a, hipStream_t st) {
+  switch (dtype) {
+    case 0: return launch_T<f16>(D, a, st);
+    case 1: return launch_T<bf16>(D, a, st);
+    case 2: return launch_T<float>(D, a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cra

@@ -1,0 +1,265 @@
+// Forward: three-phase sqrt(N) attention with one online softmax.
+//
+// Reference semantics: `_cron_root_attn_fwd_v14_tiled` (core.py:907-1158).
+// Per query i (ls = max(0, i-W+1)) the keys are the local window [ls, i]
+// (core.py:976-1028) and the global rows -- strided rows s*W < ls
+// (core.py:1042-1087) and the relay rows of blocks ending before ls
+// (core.py:1097-1142). The global rows arrive packed per block
+// (cra_global.hip), so the global set of query i is a prefix of one array and
+// both phases are dense MFMA contractions with a mask only on edge tiles
+// (the reference streams every relay row for every tile).
+// Scores are fp32 dot(q, k) * scale; P is rounded to the input dtype before
+// P.V (core.py:1027, 1086, 1141); O = acc / l and LSE = m + ln(l)
+// (core.py:1147-1158).
+//
+// Mapping: one workgroup = 4 waves = 128 consecutive queries of one (b, h);
+// each wave owns 32 queries. K/V tiles of 64 rows (32 for fp32) are staged in
+// LDS, K row-major and V transposed. S^T = K . Q^T puts a query on lane%16 so
+// the per-query softmax state is lane-local; O^T = V^T . P^T consumes P^T
+// straight from the S^T registers. Tiles are launched heaviest first (work
+// per query grows with i) and consecutive workgroups are different heads of
+// the same tile, so each XCD keeps a fixed pair of heads.
+#include "cra_common.hpp"
+#include "cra_internal.hpp"
+
+namespace cra {
+
+namespace {
+
+template <typename T, int D>
+struct FwdTraits {
+  static constexpr int kWaves = 4;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kQW = 32;                     // queries per wave
+  static constexpr int kBM = kWaves * kQW;           // queries per workgroup
+  static constexpr int kBN = sizeof(T) == 4 ? 32 : 64;  // key rows per LDS tile
+  static constexpr int kKB = kBN / 16;               // 16-row key blocks
+  static constexpr int kKC = kBN / 32;               // 32-row key chunks
+  static constexpr int kDC = D / 32;                 // 32-wide head-dim chunks
+  static constexpr int kDB = D / 16;                 // 16-wide head-dim blocks
+  static constexpr int kLD = D + 16 / (int)sizeof(T);  // row-major tile stride
+  static constexpr int kLDT = kBN + 4;               // transposed tile stride
+};
+
+// One key tile against the wave's 32 queries: S^T, masked online softmax,
+// O^T += V^T P^T. `valid(key_offset, qb)` says whether tile row key_offset is
+// in the set of query block qb's lane query.
+template <typename T, int D, bool MASK, typename Valid>
+__device__ __forceinline__ void attend_tile(const T* sK, const T* sVt,
+                                            const Frag<T> (&qf)[2][FwdTraits<T, D>::kDC],
+                                            f32x4 (&acc)[FwdTraits<T, D>::kDB][2],
+                                            float (&m_run)[2], float (&l_run)[2], float c2,
+                                            int l16, int g, Valid valid) {
+  using Tr = FwdTraits<T, D>;
+  f32x4 s[Tr::kKB][2];
+#pragma unroll
+  for (int kb = 0; kb < Tr::kKB; ++kb) {
+    s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < Tr::kDC; ++c) {
+      const Frag<T> kf = lds_frag_row<T>(sK + (16 * kb + l16) * Tr::kLD + 32 * c + 8 * g);
+      s[kb][0] = mma(s[kb][0], kf, qf[0][c]);
+      s[kb][1] = mma(s[kb][1], kf, qf[1][c]);
+    }
+  }
+  Frag<T> pf[Tr::kKC][2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float t[Tr::kKB][4];
+    float mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int kb = 0; kb < Tr::kKB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float x = s[kb][qb][r] * c2;
+        if (MASK && !valid(16 * kb + 4 * g + r, qb)) x = -__builtin_huge_valf();
+        t[kb][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = group_max(mx);
+    const float m_new = fmaxf(m_run[qb], mx);
+    const float m_use = m_new == -__builtin_huge_valf() ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < Tr::kKB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = __builtin_amdgcn_exp2f(t[kb][r] - m_use);
+        t[kb][r] = p;
+        psum += p;
+      }
+    }
+    l_run[qb] = l_run[qb] * alpha + psum;
+    m_run[qb] = m_new;
+#pragma unroll
+    for (int db = 0; db < Tr::kDB; ++db) acc[db][qb] *= alpha;
+#pragma unroll
+    for (int kc = 0; kc < Tr::kKC; ++kc) {
+      const float v8[8] = {t[2 * kc][0],     t[2 * kc][1],     t[2 * kc][2],     t[2 * kc][3],
+                           t[2 * kc + 1][0], t[2 * kc + 1][1], t[2 * kc + 1][2], t[2 * kc + 1][3]};
+      pf[kc][qb] = pack8<T>(v8);
+    }
+  }
+#pragma unroll
+  for (int db = 0; db < Tr::kDB; ++db) {
+    const T* row = sVt + (16 * db + l16) * Tr::kLDT;
+#pragma unroll
+    for (int kc = 0; kc < Tr::kKC; ++kc) {
+      const Frag<T> vf = lds_frag_2x4<T>(row + 32 * kc + 4 * g, row + 32 * kc + 16 + 4 * g);
+      acc[db][0] = mma(acc[db][0], vf, pf[kc][0]);
+      acc[db][1] = mma(acc[db][1], vf, pf[kc][1]);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
+  using Tr = FwdTraits<T, D>;
+  __shared__ __attribute__((aligned(16))) T sK[Tr::kBN * Tr::kLD];
+  __shared__ __attribute__((aligned(16))) T sVt[D * Tr::kLDT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nbh = a.B * a.Hq;
+  const int bh = blockIdx.x % nbh;
+  const int tile = a.ntiles - 1 - (int)(blockIdx.x / nbh);
+  const int b = bh / a.Hq, h = bh % a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int m0 = tile * Tr::kBM;
+  const int q0 = m0 + wave * Tr::kQW;
+  const int S = a.S, W = a.W;
+
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* gkp = static_cast<const T*>(a.gk) + gbase;
+  const T* gvp = static_cast<const T*>(a.gv) + gbase;
+
+  // Q as the B operand of S^T = K . Q^T: lane holds q[qi][32c + 8g .. +8].
+  Frag<T> qf[2][Tr::kDC];
+  int qi[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    qi[qb] = q0 + 16 * qb + l16;
+#pragma unroll
+    for (int c = 0; c < Tr::kDC; ++c) {
+      if (qi[qb] < S) {
+        qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qi[qb] * a.qss + 32 * c + 8 * g);
+      } else {
+#pragma unroll
+        for (int w = 0; w < Frag<T>::kWords; ++w) qf[qb][c].w[w] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+
+  const float c2 = a.scale * kLog2e;
+  float m_run[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
+  float l_run[2] = {0.f, 0.f};
+  f32x4 acc[Tr::kDB][2];
+#pragma unroll
+  for (int db = 0; db < Tr::kDB; ++db) acc[db][0] = acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool active = q0 < S;
+  const int q_last = min(q0 + Tr::kQW, S) - 1;
+  TileStage<T, D, Tr::kBN, Tr::kThreads> stk, stv;
+
+  // ---- phase 1: local window -------------------------------------------
+  const int lo = max(0, m0 - W + 1);
+  const int hi = min(S, m0 + Tr::kBM);
+  const int w_lo = max(0, q0 - W + 1);
+  for (int ts = lo; ts < hi; ts += Tr::kBN) {
+    stk.load(kp, a.kss, ts, 0, hi, tid);
+    stv.load(vp, a.vss, ts, 0, hi, tid);
+    __syncthreads();
+    stk.template store_rows<Tr::kLD>(sK, tid);
+    stv.template store_cols<Tr::kLDT>(sVt, tid);
+    __syncthreads();
+    if (active && ts <= q_last && ts + Tr::kBN - 1 >= w_lo) {
+      const bool full = ts >= q_last - W + 1 && ts + Tr::kBN - 1 <= q0;
+      auto valid = [&](int ko, int qb) {
+        const int j = ts + ko;
+        return j <= qi[qb] && j >= qi[qb] - W + 1;
+      };
+      if (full)
+        attend_tile<T, D, false>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+      else
+        attend_tile<T, D, true>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+    }
+  }
+
+  // ---- phase 2+3: prefix of the packed strided/relay rows ---------------
+  const int gmax = glob_prefix(hi - 1, W, a.rpb);
+  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+  for (int ts = 0; ts < gmax; ts += Tr::kBN) {
+    stk.load(gkp, D, ts, 0, gmax, tid);
+    stv.load(gvp, D, ts, 0, gmax, tid);
+    __syncthreads();
+    stk.template store_rows<Tr::kLD>(sK, tid);
+    stv.template store_cols<Tr::kLDT>(sVt, tid);
+    __syncthreads();
+    if (active && ts < wg_hi) {
+      auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
+      if (ts + Tr::kBN <= wg_lo)
+        attend_tile<T, D, false>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+      else
+        attend_tile<T, D, true>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+    }
+  }
+
+  // ---- epilogue: O = acc / l, LSE = (m + log2 l) ln 2 ---------------------
+  T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l = group_sum(l_run[qb]);
+    if (!active || qi[qb] >= S) continue;
+    const float inv = 1.f / fmaxf(l, 1e-6f);
+    T* orow = op + (int64_t)qi[qb] * a.oss;
+#pragma unroll
+    for (int db = 0; db < Tr::kDB; ++db) {
+      T e[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) e[r] = from_f32<T>(acc[db][qb][r] * inv);
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = *reinterpret_cast<const uint2*>(e);
+      } else {
+        *reinterpret_cast<uint4*>(orow + 16 * db + 4 * g) = *reinterpret_cast<const uint4*>(e);
+      }
+    }
+    if (g == 0)
+      a.lse[(int64_t)bh * S + qi[qb]] = (m_run[qb] + __builtin_amdgcn_logf(fmaxf(l, 1e-6f))) * kLn2;
+  }
+}
+
+template <typename T>
+hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
+  dim3 grid(a.ntiles * a.B * a.Hq);
+  switch (D) {
+    case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
+    case 128: hipLaunchKernelGGL((fwd_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int fwd_block_queries() { return 128; }
+
+hipError_t launch_fwd(int dtype, int D, const FwdArgs& a, hipStream_t st) {
+  switch (dtype) {
+    case 0: return launch_T<f16>(D, a, st);
+    case 1: return launch_T<bf16>(D, a, st);
+    case 2: return launch_T<float>(D, a, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cra

@@ -1,0 +1,168 @@
+// Packed global rows: per W-block, its strided row and its top_k relay rows.
+//
+// Follows the reference relay pre-computation `_relay_precompute_topk`
+// (core.py:2630-2748): per block, rank the valid rows by fp32 ||k||^2,
+// descending, the earlier row winning ties (strict '>' insertion,
+// core.py:2688-2703); a slot with no valid row left points at the block's
+// first row (core.py:2668-2669). Unlike the reference, which walks the W rows
+// of a block one at a time in a single program, one 256-thread workgroup scans
+// a block with D/8 lanes per row; every row group keeps its own sorted top-4
+// and the lists are merged with the same (norm desc, row asc) order, which
+// yields the same selection as the sequential scan.
+//
+// The squared norm of a row is summed in one fixed order so a CPU check can
+// reproduce it bit for bit: each lane sums the squares of its 8 consecutive
+// elements left to right (no fused multiply-add), then the D/8 lane partials
+// are combined by a butterfly p += p[lane ^ off], off = D/16 .. 1.
+#include "cra_common.hpp"
+#include "cra_internal.hpp"
+
+namespace cra {
+
+namespace {
+
+constexpr float kSentinel = -1e38f;  // below any squared norm
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
+  constexpr int kLPR = D / 8;        // lanes per row
+  constexpr int kNRG = 256 / kLPR;   // row groups per workgroup
+  constexpr int kW16 = Frag<T>::kWords;
+  const int r = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.Hkv, h = bh % a.Hkv;
+  const T* kb = static_cast<const T*>(a.k) + b * a.ksb + h * a.ksh;
+  const T* vb = static_cast<const T*>(a.v) + b * a.vsb + h * a.vsh;
+  const int tid = threadIdx.x;
+  const int row0 = r * a.W;
+
+  __shared__ float s_norm[kNRG * 4];
+  __shared__ int s_idx[kNRG * 4];
+  __shared__ int s_sel[4];
+
+  if (a.relay) {
+    const int li = tid % kLPR;
+    const int rg = tid / kLPR;
+    const int nrows = min(a.W, a.S - row0);
+    float bn[4] = {kSentinel, kSentinel, kSentinel, kSentinel};
+    int bi[4] = {0, 0, 0, 0};
+    for (int base = 0; base < nrows; base += kNRG) {  // uniform trip count
+      const int rr = base + rg;
+      const bool valid = rr < nrows;
+      float x[8];
+      if (valid) {
+        const uint4* p = reinterpret_cast<const uint4*>(kb + (int64_t)(row0 + rr) * a.kss + li * 8);
+        uint4 w[kW16];
+#pragma unroll
+        for (int i = 0; i < kW16; ++i) w[i] = p[i];
+        const T* e = reinterpret_cast<const T*>(w);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = to_f32(e[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = 0.f;
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = __fadd_rn(acc, __fmul_rn(x[i], x[i]));
+#pragma unroll
+      for (int off = kLPR / 2; off >= 1; off >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, off));
+      if (valid) {
+        // strict '>' cascade, rows arrive in increasing order within a group
+        const bool b0 = acc > bn[0], b1 = acc > bn[1], b2 = acc > bn[2], b3 = acc > bn[3];
+        const float n3 = b2 ? bn[2] : (b3 ? acc : bn[3]);
+        const int i3 = b2 ? bi[2] : (b3 ? rr : bi[3]);
+        const float n2 = b1 ? bn[1] : (b2 ? acc : bn[2]);
+        const int i2 = b1 ? bi[1] : (b2 ? rr : bi[2]);
+        const float n1 = b0 ? bn[0] : (b1 ? acc : bn[1]);
+        const int i1 = b0 ? bi[0] : (b1 ? rr : bi[1]);
+        bn[0] = b0 ? acc : bn[0];
+        bi[0] = b0 ? rr : bi[0];
+        bn[1] = n1; bi[1] = i1;
+        bn[2] = n2; bi[2] = i2;
+        bn[3] = n3; bi[3] = i3;
+      }
+    }
+    if (li == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s_norm[rg * 4 + j] = bn[j];
+        s_idx[rg * 4 + j] = bi[j];
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      // A taken candidate is parked at -inf, below the sentinel of unset slots.
+      for (int j = 0; j < a.top_k; ++j) {
+        int best = 0;
+        for (int c = 1; c < kNRG * 4; ++c) {
+          if (s_norm[c] > s_norm[best] || (s_norm[c] == s_norm[best] && s_idx[c] < s_idx[best]))
+            best = c;
+        }
+        s_sel[j] = row0 + s_idx[best];
+        s_norm[best] = -__builtin_huge_valf();
+      }
+      int32_t* src = a.src + (int64_t)bh * a.NB * a.top_k + (int64_t)r * a.top_k;
+      for (int j = 0; j < a.top_k; ++j) src[j] = s_sel[j];
+    }
+    __syncthreads();
+  }
+
+  // Emit rows: slot 0 = strided row r*W, slots 1..top_k = relay rows.
+  T* gk = static_cast<T*>(a.gk) + ((int64_t)bh * a.G + (int64_t)r * a.rpb) * D;
+  T* gv = static_cast<T*>(a.gv) + ((int64_t)bh * a.G + (int64_t)r * a.rpb) * D;
+  const int cg = tid % (D / 8);
+  const float sc = (a.relay && a.scale) ? a.scale[h] : 1.f;
+  for (int slot = tid / (D / 8); slot < a.rpb; slot += 256 / (D / 8)) {
+    const int row = slot == 0 ? row0 : s_sel[slot - 1];
+    const uint4* pk = reinterpret_cast<const uint4*>(kb + (int64_t)row * a.kss + cg * 8);
+    const uint4* pv = reinterpret_cast<const uint4*>(vb + (int64_t)row * a.vss + cg * 8);
+    uint4 wk[kW16], wv[kW16];
+#pragma unroll
+    for (int i = 0; i < kW16; ++i) {
+      wk[i] = pk[i];
+      wv[i] = pv[i];
+    }
+    if (slot > 0 && a.scale) {
+      T* ek = reinterpret_cast<T*>(wk);
+      T* ev = reinterpret_cast<T*>(wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ek[i] = from_f32<T>(to_f32(ek[i]) * sc);
+        ev[i] = from_f32<T>(to_f32(ev[i]) * sc);
+      }
+    }
+    uint4* dk = reinterpret_cast<uint4*>(gk + (int64_t)slot * D + cg * 8);
+    uint4* dv = reinterpret_cast<uint4*>(gv + (int64_t)slot * D + cg * 8);
+#pragma unroll
+    for (int i = 0; i < kW16; ++i) {
+      dk[i] = wk[i];
+      dv[i] = wv[i];
+    }
+  }
+}
+
+template <typename T>
+hipError_t launch_T(int D, const GlobalArgs& a, int B, hipStream_t st) {
+  dim3 grid(a.NB, B * a.Hkv);
+  switch (D) {
+    case 32: hipLaunchKernelGGL((build_global_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
+    case 64: hipLaunchKernelGGL((build_global_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
+    case 128: hipLaunchKernelGGL((build_global_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_build_global(int dtype, int D, const GlobalArgs& a, int B, hipStream_t st) {
+  switch (dtype) {
+    case 0: return launch_T<f16>(D, a, B, st);
+    case 1: return launch_T<bf16>(D, a, B, st);
+    case 2: return launch_T<float>(D, a, B, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace cra

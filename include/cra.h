@@ -1,0 +1,135 @@
+/*
+ * cra.h -- C ABI of the MI355X (gfx950) sqrt(N) sparse-attention library
+ * (libcra_hip.so).
+ *
+ * The attention computed is the reference's three-phase pattern: for query i
+ * with ls = max(0, i-W+1) the keys are the local window [ls, i], the strided
+ * rows s*W < ls, and (when relay is on) the top_k highest-||k||^2 rows of
+ * every W-block that ends before ls; one softmax runs over the multiset.
+ *
+ * Conventions (every entry point):
+ *  - Return value: 0 on success, a negative CRA_E_* code otherwise; the
+ *    message of the last failure on the calling thread is available from
+ *    cra_last_error(). No exceptions cross the ABI, no host synchronisation
+ *    happens, nothing is allocated: the caller passes every buffer.
+ *  - Tensors of shape [B, H, S, D] are passed as cra_tensor: a device pointer
+ *    and element strides for B, H and S; D must be contiguous (stride 1), the
+ *    pointer and every row start must be 16-byte aligned.
+ *  - `stream` is a hipStream_t (0 = the null stream); all work is enqueued on it.
+ *  - Concurrent calls on different streams are safe; the library keeps no
+ *    mutable global state.
+ */
+#ifndef CRA_H_
+#define CRA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CRA_ABI_VERSION 1
+
+enum {
+  CRA_OK = 0,
+  CRA_E_INVALID = -1,     /* bad shape, size or argument */
+  CRA_E_LAYOUT = -2,      /* stride/alignment the kernels cannot take */
+  CRA_E_DTYPE = -3,       /* unknown dtype code */
+  CRA_E_UNSUPPORTED = -4, /* valid but not built (e.g. head dim) */
+  CRA_E_HIP = -5,         /* HIP runtime error (launch, device query) */
+  CRA_E_WORKSPACE = -6    /* workspace missing or too small */
+};
+
+enum { CRA_F16 = 0, CRA_BF16 = 1, CRA_F32 = 2 };
+
+/* One attention problem. W, relay and top_k are the planner's choices
+ * (the reference uses W = ceil(sqrt(S)), relay = S > 2048, top_k = 2;
+ * core.py:3479, 3507, 3771). `scale` is the logit scale (1/sqrt(head dim)). */
+typedef struct {
+  int32_t B, H_q, H_kv, S, D;
+  int32_t W;
+  int32_t relay; /* 0 or 1 */
+  int32_t top_k; /* relay rows per block, 1..4 (ignored when relay == 0) */
+  int32_t dtype; /* CRA_F16, CRA_BF16 or CRA_F32 */
+  float scale;
+} cra_problem;
+
+typedef struct {
+  void* ptr;
+  int64_t sb, sh, ss; /* element strides of B, H, S; D is contiguous */
+} cra_tensor;
+
+typedef struct {
+  int32_t cu_count;
+  int32_t lds_bytes_per_cu;
+  int32_t arch_major, arch_minor; /* 9, 50 for gfx950 */
+  char arch_name[64];
+  char device_name[128];
+} cra_device_info_t;
+
+/* Head dims the kernels are built for (others: pad to one of them). */
+int cra_supported_head_dim(int32_t D);
+
+/* Rows of the packed "global" key/value array per (b, kv head):
+ * ceil(S/W) * (1 + top_k) with relay, ceil(S/W) without. Block r occupies
+ * rows r*(1+top_k) .. : first k[r*W] (its strided row), then its top_k relay
+ * rows in rank order. Query i sees exactly the prefix of length
+ * (1+top_k)*floor(ls/W) + (ls % W != 0) (relay) or ceil(ls/W) (no relay). */
+int64_t cra_global_rows(const cra_problem* p);
+
+/* Builds the packed global rows and the relay source rows.
+ *   k, v:       [B, H_kv, S, D]
+ *   glob_k/v:   contiguous [B, H_kv, cra_global_rows(p), D], dtype of k
+ *   relay_src:  contiguous int32 [B, H_kv, ceil(S/W) * top_k] (may be NULL
+ *               when relay == 0)
+ *   relay_scale: NULL, or fp32 [H_kv] multipliers applied to the relay rows
+ *               (the caller passes exp(relay_log_scale) already rounded to
+ *               the input dtype).
+ * Replaces the relay pre-computation kernel `_relay_precompute_topk`
+ * (reference core.py:2630-2748, launched at core.py:3516-3534) and the
+ * relay_log_scale multiply (core.py:3541-3544); also gathers the strided
+ * rows the reference's forward reads in place (core.py:1042-1087). */
+int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glob_k,
+                     void* glob_v, int32_t* relay_src, const float* relay_scale, void* stream);
+
+/* Forward: o [B, H_q, S, D] (dtype of q) and lse fp32 contiguous [B, H_q, S]
+ * (natural-log log-sum-exp per query). Query head h reads kv head
+ * h / (H_q / H_kv).
+ * Replaces the tiled forward `_cron_root_attn_fwd_v14_tiled`
+ * (reference core.py:907-1158, launched at core.py:3588-3610) and the
+ * persistent variant (core.py:711-900, launched at core.py:3548-3569). */
+int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+            const void* glob_k, const void* glob_v, cra_tensor o, float* lse, void* stream);
+
+/* Workspace the backward needs, in bytes (0 is possible). */
+size_t cra_bwd_workspace_bytes(const cra_problem* p);
+
+/* Backward: dq [B,H_q,S,D], dk/dv [B,H_kv,S,D] in the input dtype, given
+ * the forward's o and lse and the upstream gradient do. The gradient of the
+ * relay rows is added to their source rows (times relay_scale when given);
+ * with kv groups the kv gradients are summed over the group's query heads.
+ * If dalpha is not NULL it receives fp32 [H_kv]: sum over relay rows of
+ * dRK*RK + dRV*RV (the gradient of relay_log_scale), else it is skipped.
+ * Replaces the backward `CronRootAttentionV14Function.backward`
+ * (reference core.py:3626-3759) and its kernels: dQ (core.py:1165-1316),
+ * local dK/dV (core.py:1650-1745), strided dK/dV (core.py:1755-1889), relay
+ * dK/dV (core.py:2381-2492) and the relay scatter (core.py:2767-2815). */
+int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+            cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
+            const int32_t* relay_src, const float* relay_scale, cra_tensor dq, cra_tensor dk,
+            cra_tensor dv, float* dalpha, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device facts for get_num_sms()/get_gpu_info() (reference core.py:137-188,
+ * __init__.py:183-202). */
+int cra_device_info(int32_t device, cra_device_info_t* out);
+
+const char* cra_strerror(int32_t code);
+const char* cra_last_error(void);
+int32_t cra_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CRA_H_ */

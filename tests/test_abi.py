@@ -1,0 +1,107 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/cra.h declares, and rejects bad arguments with the documented codes
+before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cron_root_attention import _native as N
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "cra.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(cra_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert set(declared_functions()) == set(N._SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.load_library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.cra_abi_version() == N.ABI_VERSION
+
+
+def test_strerror_covers_codes():
+    lib = N.load_library()
+    for code in (0, -1, -2, -3, -4, -5, -6):
+        assert lib.cra_strerror(code) and lib.cra_strerror(code) != b"unknown error"
+    assert lib.cra_strerror(-99) == b"unknown error"
+
+
+def test_supported_head_dims():
+    lib = N.load_library()
+    assert [d for d in range(1, 300) if lib.cra_supported_head_dim(d)] == [32, 64, 128]
+
+
+def prob(**kw):
+    base = dict(B=1, H_q=4, H_kv=2, S=5000, D=128, W=71, relay=1, top_k=2, dtype=0, scale=0.088)
+    base.update(kw)
+    return N.CraProblem(**base)
+
+
+def test_global_rows():
+    lib = N.load_library()
+    nb = (5000 + 70) // 71
+    assert lib.cra_global_rows(ctypes.byref(prob())) == nb * 3
+    assert lib.cra_global_rows(ctypes.byref(prob(relay=0))) == nb
+    assert lib.cra_global_rows(ctypes.byref(prob(top_k=4))) == nb * 5
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(dtype=7), N.E_DTYPE, "dtype"),
+    (dict(D=48), N.E_UNSUPPORTED, "head dim"),
+    (dict(H_kv=3), N.E_INVALID, "multiple"),
+    (dict(W=0), N.E_INVALID, "window"),
+    (dict(W=6000), N.E_INVALID, "window"),
+    (dict(top_k=5), N.E_INVALID, "top_k"),
+    (dict(S=0), N.E_INVALID, ">= 1"),
+    (dict(scale=0.0), N.E_INVALID, "scale"),
+])
+def test_fwd_rejects_bad_problem(kw, code, msg):
+    lib = N.load_library()
+    t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    rc = lib.cra_fwd(ctypes.byref(prob(**kw)), t, t, t, 0x10000, 0x10000, t, 0x10000, None)
+    assert rc == code
+    assert msg in lib.cra_last_error().decode()
+
+
+def test_fwd_rejects_bad_layout():
+    lib = N.load_library()
+    good = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    odd_ptr = N.CraTensor(0x10002, 1 << 20, 1 << 16, 128)
+    odd_stride = N.CraTensor(0x10000, 1 << 20, 1 << 16, 130)
+    null = N.CraTensor(None, 1 << 20, 1 << 16, 128)
+    p = ctypes.byref(prob())
+    assert lib.cra_fwd(p, odd_ptr, good, good, 0x10000, 0x10000, good, 0x10000, None) == N.E_LAYOUT
+    assert lib.cra_fwd(p, good, odd_stride, good, 0x10000, 0x10000, good, 0x10000, None) == N.E_LAYOUT
+    assert lib.cra_fwd(p, good, good, null, 0x10000, 0x10000, good, 0x10000, None) == N.E_INVALID
+    assert lib.cra_fwd(p, good, good, good, 0x10000, 0x10000, good, None, None) == N.E_INVALID
+
+
+def test_bwd_rejects_small_workspace():
+    lib = N.load_library()
+    t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    p = ctypes.byref(prob())
+    need = lib.cra_bwd_workspace_bytes(p)
+    assert need > 0
+    rc = lib.cra_bwd(p, t, t, t, t, t, 0x10000, 0x10000, 0x10000, 0x10000, None, t, t, t, None,
+                     0x10000, need - 1, None)
+    assert rc == N.E_WORKSPACE and str(need) in lib.cra_last_error().decode()
+    rc = lib.cra_bwd(p, t, t, t, t, t, 0x10000, 0x10000, 0x10000, None, None, t, t, t, None,
+                     0x10000, need, None)
+    assert rc == N.E_INVALID  # relay on needs relay_src
+
+
+def test_build_global_requires_src_with_relay():
+    lib = N.load_library()
+    t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    rc = lib.cra_build_global(ctypes.byref(prob()), t, t, 0x10000, 0x10000, None, None, None)
+    assert rc == N.E_INVALID and "relay_src" in lib.cra_last_error().decode()

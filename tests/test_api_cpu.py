@@ -1,0 +1,90 @@
+"""Host-side API checks (CPU only): the reference's public names, argument
+validation, and that nothing silently computes on the CPU."""
+import pytest
+import torch
+
+import cron_root_attention as cra
+
+REFERENCE_ALL = ["cron_root_attention", "cron_root_attention_v14", "cron_root_attention_varlen",
+                 "warmup_varlen_shapes", "CronRootAttention", "CronRootMultiheadAttention",
+                 "cron_root_attention_hybrid", "CronRootAttentionHybrid", "calibrate",
+                 "get_num_sms", "get_gpu_info", "GPU_SM_MAP", "__version__"]
+
+
+def test_public_names_match_reference():
+    assert sorted(cra.__all__) == sorted(REFERENCE_ALL)
+    for n in REFERENCE_ALL:
+        assert hasattr(cra, n), n
+    assert cra.cron_root_attention is cra.cron_root_attention_v14
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    q = torch.randn(1, 2, 64, 32)
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
+        cra.cron_root_attention(q, q, q)
+
+
+@pytest.mark.parametrize("shapes,kw,exc", [
+    (((1, 2, 64, 32), (1, 2, 63, 32)), {}, ValueError),
+    (((1, 4, 64, 32), (1, 2, 64, 32)), {}, ValueError),            # kv_groups missing
+    (((1, 4, 64, 32), (1, 2, 64, 32)), {"kv_groups": 3}, ValueError),
+    (((2, 64, 32), (2, 64, 32)), {}, ValueError),
+])
+def test_shape_validation(shapes, kw, exc):
+    q = torch.randn(*shapes[0])
+    k = torch.randn(*shapes[1])
+    with pytest.raises(exc):
+        cra.cron_root_attention(q, k, k, **kw)
+
+
+def test_dtype_validation():
+    q = torch.randn(1, 1, 8, 32, dtype=torch.float64)
+    with pytest.raises(TypeError):
+        cra.cron_root_attention(q, q, q)
+    k = torch.randn(1, 1, 8, 32, dtype=torch.float16)
+    with pytest.raises(TypeError):
+        cra.cron_root_attention(q.float(), k, k)
+
+
+def test_varlen_validates_boundaries():
+    q = torch.randn(1, 2, 100, 32)
+    with pytest.raises(ValueError):
+        cra.cron_root_attention_varlen(q, q, q, [0, 50, 99])
+    with pytest.raises(ValueError):
+        cra.cron_root_attention_varlen(q, q, q, [0, 60, 50, 100])
+
+
+def test_hybrid_below_threshold_is_sdpa_on_any_device():
+    q = torch.randn(1, 2, 64, 32)
+    out = cra.cron_root_attention_hybrid(q, q, q, backend="auto", threshold=1024)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, q, q, is_causal=True)
+    assert torch.equal(out, ref)
+    with pytest.raises(RuntimeError):
+        cra.cron_root_attention_hybrid(q, q, q, backend="cron_root")
+    with pytest.raises(ValueError):
+        cra.cron_root_attention_hybrid(q, q, q, backend="flash")
+
+
+def test_module_hybrid_flag_routes_short_sequences_to_sdpa():
+    torch.manual_seed(0)
+    m = cra.CronRootAttention(d_model=64, n_heads=2, n_kv_heads=1, hybrid=True, threshold=128)
+    x = torch.randn(1, 32, 64)
+    y = m(x)
+    assert y.shape == x.shape
+    m2 = cra.CronRootAttention(d_model=64, n_heads=2, hybrid=False)
+    with pytest.raises(RuntimeError):
+        m2(x)
+
+
+def test_head_dim_limit():
+    from cron_root_attention.core import _padded_head_dim
+    assert [_padded_head_dim(d) for d in (1, 16, 32, 33, 64, 65, 128)] == [32, 32, 32, 64, 64, 128, 128]
+    with pytest.raises(NotImplementedError):
+        _padded_head_dim(129)
+
+
+def test_gpu_info_without_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    assert cra.get_gpu_info() == {"gpu_name": "No GPU", "sm_count": 0, "is_known_gpu": False}
+    assert cra.get_num_sms() == 1

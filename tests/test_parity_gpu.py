@@ -1,0 +1,292 @@
+"""HIP vs the CPU oracle on identical seeded inputs (GPU).
+
+Tolerances (stated by the north star for fp16; bf16/fp32 scaled to their
+precision):
+  forward  max |o - o_ref|          fp16 2e-3, bf16 3e-2, fp32 2e-5
+  backward ||g - g_ref|| / ||g_ref|| fp16 1e-2, bf16 3e-2, fp32 1e-4
+The oracle runs in fp64 on the inputs already rounded to the test dtype.
+Relay selection and the packed global rows are compared bit for bit.
+"""
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import cron_root_attention as cra
+from cron_root_attention import _native
+from cron_root_attention.core import _attention_with_plan
+from oracle import cra_oracle as O
+from tests.golden.make_golden import SHAPES, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
+TOL_FWD = {F16: 2e-3, BF16: 3e-2, F32: 2e-5}
+TOL_GRAD = {F16: 1e-2, BF16: 3e-2, F32: 1e-4}
+DEV = "cuda"
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def rand(shape, dtype, gen):
+    return torch.randn(*shape, generator=gen, dtype=torch.float32).to(dtype)
+
+
+def inputs(B, Hq, Hkv, S, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = rand((B, Hq, S, D), dtype, g)
+    k = rand((B, Hkv, S, D), dtype, g)
+    v = rand((B, Hkv, S, D), dtype, g)
+    do = rand((B, Hq, S, D), dtype, g)
+    return q, k, v, do
+
+
+def plan_for(S, top_k=2):
+    return O.Plan(S, O.window_size(S), S > 2048, top_k)
+
+
+def max_abs(a, b):
+    return float((a.detach().cpu().double() - b.detach().cpu().double()).abs().max())
+
+
+def rel_fro(a, b):
+    a = a.detach().cpu().double()
+    b = b.detach().cpu().double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+# ------------------------------------------------------------------ relay rows
+
+@pytest.mark.parametrize("dtype,S,D,top_k,scaled", [
+    (F16, 2049, 128, 2, False), (F16, 4096, 64, 2, True), (BF16, 3000, 128, 4, False),
+    (F32, 2500, 32, 3, True), (F16, 10001, 128, 1, False), (F16, 700, 64, 2, False),
+])
+def test_global_rows_bit_exact(dtype, S, D, top_k, scaled):
+    say(f"global rows {dtype} S={S} D={D} top_k={top_k} scaled={scaled}")
+    B, H = 2, 3
+    q, k, v, _ = inputs(B, H, H, S, D, dtype, seed=S + D)
+    plan = O.Plan(S, O.window_size(S), True, top_k)
+    p = _native.problem(B, H, H, S, D, plan.W, True, top_k, dtype, 1 / math.sqrt(D))
+    rs = None
+    if scaled:
+        rs = torch.tensor([0.5, 1.25, 2.0]).to(dtype).to(F32)
+    gk, gv, src = _native.build_global(p, k.to(DEV), v.to(DEV), rs.to(DEV) if rs is not None else None)
+    torch.cuda.synchronize()
+    ref_src = O.relay_select(k, plan, "lanetree").to(torch.int32)
+    assert torch.equal(src.cpu(), ref_src)
+    for b in range(B):
+        for h in range(H):
+            rows = O.packed_rows(plan, ref_src[b, h].view(-1, top_k).tolist())
+            ek, ev = k[b, h, rows].clone(), v[b, h, rows].clone()
+            if scaled:
+                relay = torch.tensor([i % (1 + top_k) != 0 for i in range(len(rows))])
+                ek[relay] = (ek[relay].float() * rs[h]).to(dtype)
+                ev[relay] = (ev[relay].float() * rs[h]).to(dtype)
+            assert torch.equal(gk[b, h].cpu(), ek)
+            assert torch.equal(gv[b, h].cpu(), ev)
+
+
+def test_global_rows_no_relay_are_strided_rows():
+    S, D = 1500, 64
+    q, k, v, _ = inputs(1, 2, 2, S, D, F16, 1)
+    W = O.window_size(S)
+    p = _native.problem(1, 2, 2, S, D, W, False, 2, F16, 0.125)
+    gk, gv, src = _native.build_global(p, k.to(DEV), v.to(DEV), None)
+    assert src is None
+    idx = torch.arange(0, S, W)
+    assert torch.equal(gk.cpu(), k[:, :, idx]) and torch.equal(gv.cpu(), v[:, :, idx])
+
+
+# --------------------------------------------------------------------- forward
+
+FWD_CASES = [
+    # dtype, B, Hq, Hkv, S, D, top_k
+    (F16, 1, 2, 2, 1, 128, 2), (F16, 1, 2, 2, 2, 128, 2), (F16, 2, 2, 2, 63, 64, 2),
+    (F16, 1, 3, 3, 129, 128, 2), (F16, 1, 2, 2, 300, 32, 2), (F16, 1, 2, 2, 2048, 128, 2),
+    (F16, 1, 2, 2, 2049, 128, 2), (F16, 1, 4, 2, 4097, 128, 2), (F16, 1, 4, 1, 3000, 64, 1),
+    (F16, 1, 2, 2, 5000, 128, 3), (F16, 1, 2, 2, 2500, 64, 4), (BF16, 1, 2, 2, 4096, 128, 2),
+    (BF16, 1, 2, 2, 1000, 64, 2), (F32, 1, 2, 2, 4096, 64, 2), (F32, 1, 2, 2, 777, 128, 2),
+    (F32, 1, 2, 2, 3001, 32, 2), (F16, 1, 2, 2, 16, 16, 2), (F16, 1, 2, 2, 2100, 80, 2),
+    (BF16, 1, 2, 1, 3333, 96, 2),
+]
+
+
+def hip_fwd_with_lse(q, k, v, plan, kv_groups=1):
+    B, Hq, S, D = q.shape
+    p = _native.problem(B, Hq, k.shape[1], S, D, plan.W, plan.relay, plan.top_k, q.dtype,
+                        1 / math.sqrt(D))
+    gk, gv, src = _native.build_global(p, k, v, None)
+    return _native.forward(p, q, k, v, gk, gv)
+
+
+@pytest.mark.parametrize("case", FWD_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_forward_matches_oracle(case):
+    dtype, B, Hq, Hkv, S, D, top_k = case
+    say(f"forward {case}")
+    q, k, v, _ = inputs(B, Hq, Hkv, S, D, dtype, seed=S * 7 + D)
+    o = cra.cron_root_attention(q.to(DEV), k.to(DEV), v.to(DEV), kv_groups=Hq // Hkv,
+                                relay_top_k=top_k)
+    ref, ref_lse, _ = O.forward(q, k, v, plan_for(S, top_k), kv_groups=Hq // Hkv)
+    assert o.shape == q.shape and o.dtype == dtype
+    err = max_abs(o, ref)
+    say(f"  max|o-ref| = {err:.3e}")
+    assert err <= TOL_FWD[dtype]
+    if D in (32, 64, 128):
+        _, lse = hip_fwd_with_lse(q.to(DEV), k.to(DEV), v.to(DEV), plan_for(S, top_k), Hq // Hkv)
+        tol = 1e-3 if dtype != F32 else 1e-5
+        assert max_abs(lse, ref_lse) <= tol
+
+
+def test_forward_strided_views_and_relay_scale():
+    say("forward strided views + relay_log_scale")
+    B, S, H, D = 1, 3000, 4, 64
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(B, S, 3, H, D, generator=g).to(F16)
+    q, k, v = (x[:, :, i].transpose(1, 2) for i in range(3))     # [B, H, S, D] views
+    alpha = torch.tensor([0.2, -0.1, 0.0, 0.4])
+    xd = x.to(DEV)
+    o = cra.cron_root_attention(xd[:, :, 0].transpose(1, 2), xd[:, :, 1].transpose(1, 2),
+                                xd[:, :, 2].transpose(1, 2), relay_log_scale=alpha.to(DEV))
+    rs = alpha.exp().to(F16).to(F32)
+    ref, _, _ = O.forward(q, k, v, plan_for(S), relay_scale=rs)
+    assert max_abs(o, ref) <= TOL_FWD[F16]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_forward_matches_reference_golden(shape):
+    """cpu_reference semantics (floor window, relay on) vs the reference's own outputs."""
+    say(f"golden {shape}")
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden",
+                             "cra_cpu_fast_B%d_H%d_S%d_D%d.npz" % shape))
+    q, k, v, _ = make_inputs(*shape)
+    plan = O.make_plan(shape[2], "cpu_reference")
+    o = _attention_with_plan(q.to(DEV), k.to(DEV), v.to(DEV), window=plan.W, relay=True)
+    rows = torch.from_numpy(z["rows"])
+    err = float((o.cpu()[:, :, rows] - torch.from_numpy(z["o_rows"])).abs().max())
+    say(f"  max|o-golden| = {err:.3e}")
+    assert err <= 2e-5
+    assert np.abs(o.double().sum(dim=(2, 3)).cpu().numpy() - z["o_sum"]).max() < 1e-2
+
+
+def test_config1_public_api_matches_golden():
+    shape = (1, 8, 4096, 64)
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden",
+                             "cra_cpu_fast_B1_H8_S4096_D64.npz"))
+    q, k, v, _ = make_inputs(*shape)
+    o = cra.cron_root_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    rows = torch.from_numpy(z["rows"])
+    assert float((o.cpu()[:, :, rows] - torch.from_numpy(z["o_rows"])).abs().max()) <= 2e-5
+
+
+# -------------------------------------------------------------------- backward
+
+BWD_CASES = [
+    (F16, 1, 2, 2, 100, 64, 2), (F16, 1, 2, 2, 2049, 128, 2), (F16, 1, 4, 2, 3000, 128, 2),
+    (BF16, 1, 2, 2, 2500, 64, 2), (F32, 1, 2, 2, 1500, 32, 2), (F32, 1, 2, 2, 4096, 64, 3),
+    (F16, 2, 2, 2, 700, 128, 2), (F16, 1, 2, 2, 2600, 80, 2), (F16, 1, 4, 1, 5000, 64, 2),
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_backward_matches_oracle(case):
+    dtype, B, Hq, Hkv, S, D, top_k = case
+    say(f"backward {case}")
+    q, k, v, do = inputs(B, Hq, Hkv, S, D, dtype, seed=S * 3 + D)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    o = cra.cron_root_attention(qd, kd, vd, kv_groups=Hq // Hkv, relay_top_k=top_k)
+    o.backward(do.to(DEV))
+    _, _, _, g = O.forward_backward(q, k, v, do, plan_for(S, top_k), kv_groups=Hq // Hkv)
+    for name, hip, ref in (("dq", qd.grad, g["dq"]), ("dk", kd.grad, g["dk"]),
+                           ("dv", vd.grad, g["dv"])):
+        e = rel_fro(hip, ref)
+        say(f"  {name}: rel = {e:.3e}")
+        assert e <= TOL_GRAD[dtype], name
+
+
+def test_backward_relay_log_scale():
+    say("backward relay_log_scale")
+    B, H, S, D = 1, 2, 3000, 64
+    q, k, v, do = inputs(B, H, H, S, D, F32, seed=5)
+    alpha = torch.tensor([0.3, -0.25])
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    ad = alpha.to(DEV).requires_grad_(True)
+    o = cra.cron_root_attention(qd, kd, vd, relay_log_scale=ad)
+    o.backward(do.to(DEV))
+    _, _, _, g = O.forward_backward(q, k, v, do, plan_for(S), relay_log_scale=alpha)
+    assert rel_fro(qd.grad, g["dq"]) <= 1e-4
+    assert rel_fro(kd.grad, g["dk"]) <= 1e-4
+    assert rel_fro(vd.grad, g["dv"]) <= 1e-4
+    assert rel_fro(ad.grad, g["dalpha"]) <= 1e-4
+
+
+def test_backward_deterministic():
+    B, H, S, D = 1, 4, 6000, 128
+    q, k, v, do = inputs(B, H, H, S, D, F16, seed=9)
+    grads = []
+    for _ in range(2):
+        qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+        cra.cron_root_attention(qd, kd, vd).backward(do.to(DEV))
+        grads.append((qd.grad.clone(), kd.grad.clone(), vd.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+# ------------------------------------------------- north-star size (ns) checks
+
+def ns_inputs(dtype=F16):
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    shape = (1, 16, 131072, 128)
+    q = torch.randn(*shape, generator=gen, device=DEV, dtype=torch.float32).to(dtype)
+    k = torch.randn(*shape, generator=gen, device=DEV, dtype=torch.float32).to(dtype)
+    v = torch.randn(*shape, generator=gen, device=DEV, dtype=torch.float32).to(dtype)
+    return q, k, v
+
+
+def test_ns_forward_rows_and_relay_selection():
+    say("ns forward spot rows")
+    q, k, v = ns_inputs()
+    S = q.shape[2]
+    plan = plan_for(S)
+    o = cra.cron_root_attention(q, k, v)
+    p = _native.problem(1, 16, 16, S, 128, plan.W, True, 2, F16, 1 / math.sqrt(128))
+    _, _, src = _native.build_global(p, k, v, None)
+    kc = k.cpu()
+    assert torch.equal(src.cpu(), O.relay_select(kc, plan, "lanetree").to(torch.int32))
+    heads = [0, 15]
+    qc, vc, oc = q.cpu()[:, heads], v.cpu()[:, heads], o.cpu()[:, heads]
+    kh = kc[:, heads]
+    srch = src.cpu()[:, heads].long()
+    for lo, hi in ((0, 256), (65536, 65792), (S - 256, S)):
+        ref, _, _ = O.forward(qc, kh, vc, plan, src=srch, rows=(lo, hi))
+        err = max_abs(oc[:, :, lo:hi], ref)
+        say(f"  rows [{lo},{hi}) max err {err:.3e}")
+        assert err <= TOL_FWD[F16]
+
+
+def test_ns_backward_identities_and_determinism():
+    """sum_j dV_j = sum_i dO_i and sum_j dK_j = 0 hold for any softmax
+    attention; they check every gradient path at the full size."""
+    say("ns backward identities")
+    q, k, v = ns_inputs()
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    do = torch.randn(q.shape, generator=gen, device=DEV, dtype=torch.float32).to(F16)
+    res = []
+    for _ in range(2):
+        qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+        cra.cron_root_attention(qd, kd, vd).backward(do)
+        res.append((qd.grad, kd.grad, vd.grad))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    dq, dk, dv = res[0]
+    sdv = dv.double().sum(2)
+    sdo = do.double().sum(2)
+    assert float((sdv - sdo).abs().max()) <= 1e-3 * float(sdo.abs().max()) + 0.5
+    sdk = dk.double().sum(2)
+    assert float(sdk.abs().max()) <= 1e-2 * float(dk.double().abs().sum(2).max())
+    assert torch.isfinite(dq).all() and torch.isfinite(dk).all() and torch.isfinite(dv).all()
