@@ -71,36 +71,28 @@ def timed(fn, steps, warmup, torch):
 
 
 def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
-    """Oracle CPU port (fp32) on sampled 256-query chunks, spread evenly over
-    the sequence, until ~budget_s of CPU time; returns TFLOP/s."""
-    import numpy as np
+    """Oracle CPU port (fp32 forward) on the host cores: pairs of heads of the
+    same workload, each over all S queries, until ~budget_s of CPU time (or
+    all H heads); returns effective TFLOP/s over the rows done."""
     import torch
     from oracle import cra_oracle as O
     from oracle.cpu_port import cra_cpu_chunked
     torch.set_num_threads(threads)
-    g = torch.Generator().manual_seed(0)
-    Hs = 2  # heads held in host memory for the sample
-    q = torch.randn(1, Hs, S, D, generator=g)
-    k = torch.randn(1, Hs, S, D, generator=g)
-    v = torch.randn(1, Hs, S, D, generator=g)
     plan = O.make_plan(S)
-    src = O.relay_select(k, plan, "lanetree")
-    n_chunks = S // 256
-    order = np.random.default_rng(0).permutation(n_chunks)
-    done_rows = []
-    t_used = 0.0
-    for c in order:
-        lo = int(c) * 256
+    Hs = 2
+    t_used, heads_done, flops = 0.0, 0, 0
+    g = torch.Generator().manual_seed(0)
+    while heads_done < H and t_used < budget_s:
+        q, k, v = (torch.randn(1, Hs, S, D, generator=g) for _ in range(3))
+        src = O.relay_select(k, plan, "lanetree")
         t0 = time.perf_counter()
-        cra_cpu_chunked(q, k, v, plan, src=src, q_rows=(lo, lo + 256))
+        cra_cpu_chunked(q, k, v, plan, src=src)
         t_used += time.perf_counter() - t0
-        done_rows.extend(range(lo, lo + 256))
-        if t_used >= budget_s:
-            break
-    flops = 4 * D * row_pairs(done_rows, S) * Hs
+        heads_done += Hs
+        flops += 4 * D * pairs_fast(S) * Hs
     return {"value": flops / t_used / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"fp32 forward, {len(done_rows) // 256} random 256-query chunks x {Hs} heads "
-                      f"of S={S}, D={D} ({len(done_rows) * Hs} query rows, {t_used:.1f} s)",
+            "sample": f"fp32 forward of {heads_done} of {H} heads (all {S} queries each), "
+                      f"D={D}, {t_used:.1f} s",
             "seconds": round(t_used, 2)}
 
 
