@@ -87,9 +87,11 @@ def _padded_head_dim(D: int) -> int:
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
-    """d contiguous, 16-byte aligned rows; otherwise a contiguous copy."""
+    """d contiguous, 16-byte aligned rows, one head within 2 GiB (the kernels
+    address a head with 32-bit byte offsets); otherwise a contiguous copy."""
     vec = 16 // t.element_size()
-    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0
+    span = ((t.shape[2] - 1) * t.stride(2) + t.shape[3]) * t.element_size()
+    ok = (t.stride(3) == 1 and t.data_ptr() % 16 == 0 and span < (1 << 31)
           and all(s % vec == 0 for s in t.stride()[:3]))
     return t if ok else t.contiguous()
 

@@ -62,6 +62,15 @@ int check_tensor(const char* name, const cra_tensor& t, int esz) {
   return CRA_OK;
 }
 
+// Kernels address one (b, h) slice with 32-bit byte offsets.
+int check_span(const char* name, const cra_tensor& t, const cra_problem* p, int esz) {
+  const int64_t span = ((int64_t)(p->S - 1) * t.ss + p->D) * esz;
+  if (span >= ((int64_t)1 << 31))
+    return fail(CRA_E_LAYOUT, "%s: one head spans %lld bytes (limit 2^31); pass a contiguous tensor",
+                name, (long long)span);
+  return CRA_OK;
+}
+
 int check_buf(const char* name, const void* p) {
   if (!p) return fail(CRA_E_INVALID, "%s: NULL pointer", name);
   if (reinterpret_cast<uintptr_t>(p) % 16)
@@ -125,6 +134,8 @@ int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cons
   if (int e = check_tensor("k", k, esz)) return e;
   if (int e = check_tensor("v", v, esz)) return e;
   if (int e = check_tensor("o", o, esz)) return e;
+  if (int e = check_span("k", k, p, esz)) return e;
+  if (int e = check_span("v", v, p, esz)) return e;
   if (int e = check_buf("glob_k", glob_k)) return e;
   if (int e = check_buf("glob_v", glob_v)) return e;
   if (int e = check_buf("lse", lse)) return e;

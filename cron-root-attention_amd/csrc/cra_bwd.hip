@@ -20,6 +20,8 @@
 //                        writes dK/dV once.
 // No atomics: every output row has exactly one writer and the partial sums
 // are reduced in a fixed order, so two runs give identical bits.
+#include <type_traits>
+
 #include "cra_common.hpp"
 #include "cra_internal.hpp"
 
@@ -569,6 +571,478 @@ __global__ __launch_bounds__(256) void dalpha_kernel(BwdArgs a) {
   if (tid == 0) a.dalpha[hk] = red[0];
 }
 
+// ---------------------------------------------------------------------------
+// fp16/bf16 backward kernels on the gfx950 tile machinery (see SwzTile):
+// K/V (dq2) or Q/dO (dkdv2) tiles of 64 rows double-buffered in swizzled LDS,
+// filled by buffer loads straight into LDS while the previous tile is
+// computed; transposed operands (K^T for dQ, Q^T and dO^T for dK/dV) are
+// read with ds_read_b64_tr_b16 from the same row-major tiles.
+// ---------------------------------------------------------------------------
+template <int D>
+struct LaneOffs {
+  int row[D / 32];  // row fragment, chunk 4c + g, row lane%16
+  int tr[D / 16];   // transposed fragment, columns 16 db ..
+};
+
+template <int D>
+__device__ __forceinline__ LaneOffs<D> lane_offs(int lane) {
+  using Tile = SwzTile<D, 64>;
+  LaneOffs<D> o;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) o.row[c] = Tile::row_lane_off(lane, 4 * c + g);
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) o.tr[db] = Tile::tr_lane_off(lane, 16 * db);
+  return o;
+}
+
+template <typename T, int D, bool MASK, typename Valid>
+__device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const LaneOffs<D>& lo,
+                                         const Frag<T> (&qf)[2][D / 32],
+                                         const Frag<T> (&df)[2][D / 32], f32x4 (&dqa)[D / 16][2],
+                                         const float (&lse2)[2], const float (&dl)[2], float c2,
+                                         int g, Valid valid) {
+  using Tile = SwzTile<D, 64>;
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    float ds[2][2][4];  // [h][qb][r]
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kb = 2 * kc + h;
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, p0 = s0, p1 = s0;
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.row[c]);
+        const Frag<T> vf = Tile::template row_frag_at<T>(tV + kb * Tile::kBlk16 + lo.row[c]);
+        s0 = mma(s0, kf, qf[0][c]);
+        s1 = mma(s1, kf, qf[1][c]);
+        p0 = mma(p0, vf, df[0][c]);
+        p1 = mma(p1, vf, df[1][c]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ko = 16 * kb + 4 * g + r;
+        float x0 = fmaf(s0[r], c2, -lse2[0]);
+        float x1 = fmaf(s1[r], c2, -lse2[1]);
+        if (MASK) {
+          if (!valid(ko, 0)) x0 = -__builtin_huge_valf();
+          if (!valid(ko, 1)) x1 = -__builtin_huge_valf();
+        }
+        ds[h][0][r] = __builtin_amdgcn_exp2f(x0) * (p0[r] - dl[0]);
+        ds[h][1][r] = __builtin_amdgcn_exp2f(x1) * (p1[r] - dl[1]);
+      }
+    }
+    Frag<T> dsf[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const float v8[8] = {ds[0][qb][0], ds[0][qb][1], ds[0][qb][2], ds[0][qb][3],
+                           ds[1][qb][0], ds[1][qb][1], ds[1][qb][2], ds[1][qb][3]};
+      dsf[qb] = pack8<T>(v8);
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      const char* pa = tK + (2 * kc) * Tile::kBlk16 + lo.tr[db];
+      const Frag<T> kt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+      dqa[db][0] = mma(dqa[db][0], kt, dsf[0]);
+      dqa[db][1] = mma(dqa[db][1], kt, dsf[1]);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void dq2_kernel(BwdArgs a, int ntiles) {
+  using Tile = SwzTile<D, 64>;
+  constexpr int kBM = 128, kQW = 32, kBN = 64;
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nbh = a.B * a.Hq;
+  const int bh = blockIdx.x % nbh;
+  const int tile = ntiles - 1 - (int)(blockIdx.x / nbh);
+  const int b = bh / a.Hq, h = bh % a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int m0 = tile * kBM;
+  const int q0 = m0 + wave * kQW;
+  const int S = a.S, W = a.W;
+
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+  const T* dop = static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* gkp = static_cast<const T*>(a.gk) + gbase;
+  const T* gvp = static_cast<const T*>(a.gv) + gbase;
+
+  const int lo_k = max(0, m0 - W + 1);
+  const int hi = min(S, m0 + kBM);
+  const int gmax = glob_prefix(hi - 1, W, a.rpb);
+  const int nloc = (hi - lo_k + kBN - 1) / kBN;
+  const int ntot = nloc + (gmax + kBN - 1) / kBN;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((S - 1) * a.kss * 2 + D * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((S - 1) * a.vss * 2 + D * 2));
+  const __amdgpu_buffer_rsrc_t rgk = make_rsrc(gkp, (uint32_t)(a.G * D * 2));
+  const __amdgpu_buffer_rsrc_t rgv = make_rsrc(gvp, (uint32_t)(a.G * D * 2));
+  const int kbytes = (int)(a.kss * 2), vbytes = (int)(a.vss * 2);
+  auto issue = [&](int it, char* dst) {
+    if (it < nloc) {
+      const int ts = lo_k + it * kBN;
+      Tile::template load<4>(dst, rk, kbytes, ts, 0, hi, wave, lane);
+      Tile::template load<4>(dst + Tile::kBytes, rv, vbytes, ts, 0, hi, wave, lane);
+    } else {
+      const int ts = (it - nloc) * kBN;
+      Tile::template load<4>(dst, rgk, D * 2, ts, 0, gmax, wave, lane);
+      Tile::template load<4>(dst + Tile::kBytes, rgv, D * 2, ts, 0, gmax, wave, lane);
+    }
+  };
+  issue(0, lds[0][0]);
+
+  const LaneOffs<D> lo = lane_offs<D>(lane);
+  Frag<T> qf[2][D / 32], df[2][D / 32];
+  int qi[2];
+  float lse2[2], dl[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    qi[qb] = q0 + 16 * qb + l16;
+    const bool ok = qi[qb] < S;
+    lse2[qb] = ok ? a.lse[(int64_t)bh * S + qi[qb]] * kLog2e : 0.f;
+    dl[qb] = ok ? a.delta[(int64_t)bh * S + qi[qb]] : 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      if (ok) {
+        qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qi[qb] * a.qss + 32 * c + 8 * g);
+        df[qb][c] = lds_frag_row<T>(dop + (int64_t)qi[qb] * a.doss + 32 * c + 8 * g);
+      } else {
+        zero_frag(qf[qb][c]);
+        zero_frag(df[qb][c]);
+      }
+    }
+  }
+  const float c2 = a.scale * kLog2e;
+  f32x4 dqa[D / 16][2];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) dqa[db][0] = dqa[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool active = q0 < S;
+  const int q_last = min(q0 + kQW, S) - 1;
+  const int w_lo = max(0, q0 - W + 1);
+  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+
+  auto step = [&](auto BUFC, int it) {
+    constexpr int BUF = decltype(BUFC)::value;
+    wait_vmem();
+    __syncthreads();
+    if (it + 1 < ntot) issue(it + 1, lds[BUF ^ 1][0]);
+    const char* tK = lds[BUF][0];
+    const char* tV = lds[BUF][1];
+    if (it < nloc) {
+      const int ts = lo_k + it * kBN;
+      if (active && ts <= q_last && ts + kBN - 1 >= w_lo) {
+        auto valid = [&](int ko, int qb) {
+          const int j = ts + ko;
+          return j <= qi[qb] && j >= qi[qb] - W + 1;
+        };
+        if (ts >= q_last - W + 1 && ts + kBN - 1 <= q0)
+          dq2_tile<T, D, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
+        else
+          dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
+      }
+    } else {
+      const int ts = (it - nloc) * kBN;
+      if (active && ts < wg_hi) {
+        auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
+        if (ts + kBN <= wg_lo)
+          dq2_tile<T, D, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
+        else
+          dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
+      }
+    }
+  };
+  for (int it = 0; it < ntot; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
+  }
+
+  T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    if (!active || qi[qb] >= S) continue;
+    T* row = dqp + (int64_t)qi[qb] * a.dqss;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) store4<T>(row + 16 * db + 4 * g, dqa[db][qb], a.scale);
+  }
+}
+
+// Key-centric dK/dV: each wave owns 32 key rows (rows of k/v, or packed
+// global rows with GLOB), B operands in registers; query tiles of 64 rows of
+// Q and dO stream through LDS with their LSE and Delta. A key row j sees the
+// queries [j, j+W-1] (local) or [first_query(j), S) (global rows), so every
+// mask is a per-key interval.
+template <typename T, int D, bool MASK>
+__device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const float* sL,
+                                           const float* sDl, const LaneOffs<D>& lo,
+                                           const Frag<T> (&kf)[2][D / 32],
+                                           const Frag<T> (&vf)[2][D / 32],
+                                           f32x4 (&dka)[D / 16][2], f32x4 (&dva)[D / 16][2],
+                                           float c2, int g, int ts, const int (&qmin)[2],
+                                           const int (&qmax)[2]) {
+  using Tile = SwzTile<D, 64>;
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    float p[2][2][4], ds[2][2][4];  // [qb2][kb][r]
+#pragma unroll
+    for (int qb2 = 0; qb2 < 2; ++qb2) {
+      const int qblk = 2 * qs + qb2;
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, d0 = s0, d1 = s0;
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const Frag<T> qa = Tile::template row_frag_at<T>(tQ + qblk * Tile::kBlk16 + lo.row[c]);
+        const Frag<T> oa = Tile::template row_frag_at<T>(tO + qblk * Tile::kBlk16 + lo.row[c]);
+        s0 = mma(s0, qa, kf[0][c]);
+        s1 = mma(s1, qa, kf[1][c]);
+        d0 = mma(d0, oa, vf[0][c]);
+        d1 = mma(d1, oa, vf[1][c]);
+      }
+      const f32x4 lq = *reinterpret_cast<const f32x4*>(sL + 16 * qblk + 4 * g) * kLog2e;
+      const f32x4 dq = *reinterpret_cast<const f32x4*>(sDl + 16 * qblk + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qabs = ts + 16 * qblk + 4 * g + r;
+        float x0 = fmaf(s0[r], c2, -lq[r]);
+        float x1 = fmaf(s1[r], c2, -lq[r]);
+        if (MASK) {
+          if (qabs < qmin[0] || qabs > qmax[0]) x0 = -__builtin_huge_valf();
+          if (qabs < qmin[1] || qabs > qmax[1]) x1 = -__builtin_huge_valf();
+        }
+        p[qb2][0][r] = __builtin_amdgcn_exp2f(x0);
+        p[qb2][1][r] = __builtin_amdgcn_exp2f(x1);
+        ds[qb2][0][r] = p[qb2][0][r] * (d0[r] - dq[r]);
+        ds[qb2][1][r] = p[qb2][1][r] * (d1[r] - dq[r]);
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const float pv[8] = {p[0][kb][0], p[0][kb][1], p[0][kb][2], p[0][kb][3],
+                           p[1][kb][0], p[1][kb][1], p[1][kb][2], p[1][kb][3]};
+      const float sv[8] = {ds[0][kb][0], ds[0][kb][1], ds[0][kb][2], ds[0][kb][3],
+                           ds[1][kb][0], ds[1][kb][1], ds[1][kb][2], ds[1][kb][3]};
+      const Frag<T> pf = pack8<T>(pv);
+      const Frag<T> sf = pack8<T>(sv);
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        const char* po = tO + (2 * qs) * Tile::kBlk16 + lo.tr[db];
+        const char* pq = tQ + (2 * qs) * Tile::kBlk16 + lo.tr[db];
+        const Frag<T> ot = Tile::template tr_frag_at<T>(po, po + Tile::kBlk16);
+        const Frag<T> qt = Tile::template tr_frag_at<T>(pq, pq + Tile::kBlk16);
+        dva[db][kb] = mma(dva[db][kb], ot, pf);
+        dka[db][kb] = mma(dka[db][kb], qt, sf);
+      }
+    }
+  }
+}
+
+template <typename T, int D, bool GLOB>
+__global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
+  using Tile = SwzTile<D, 64>;
+  constexpr int kBK = 128, kKW = 32, kBQ = 64;
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
+  __shared__ __attribute__((aligned(16))) float sLD[2][2][kBQ];  // [buf][lse2, delta][q]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nbh = a.B * a.Hkv;
+  const int bhk = blockIdx.x % nbh;
+  const int rest = blockIdx.x / nbh;
+  const int chunk = GLOB ? rest % a.nchunk : 0;
+  const int tile = GLOB ? rest / a.nchunk : rest;
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int grp = a.Hq / a.Hkv;
+  const int S = a.S, W = a.W;
+  const int nrows = GLOB ? (int)a.G : S;
+  const int k0 = tile * kBK;
+  const int kw = k0 + wave * kKW;
+
+  const T* kbase;
+  const T* vbase;
+  int64_t kstride, vstride;
+  if (GLOB) {
+    const int64_t gb = (int64_t)bhk * a.G * D;
+    kbase = static_cast<const T*>(a.gk) + gb;
+    vbase = static_cast<const T*>(a.gv) + gb;
+    kstride = D;
+    vstride = D;
+  } else {
+    kbase = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+    vbase = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+    kstride = a.kss;
+    vstride = a.vss;
+  }
+
+  // query interval of the workgroup; per-key intervals for the masks
+  int q_lo, q_hi;
+  if (GLOB) {
+    const int c_lo = chunk * a.chunk_len;
+    q_hi = min(S, c_lo + a.chunk_len);
+    q_lo = max(c_lo, glob_row_first_query(k0, W, a.rpb));
+  } else {
+    q_lo = k0;
+    q_hi = min(S, k0 + kBK - 1 + W);
+  }
+  const int ntile_q = q_hi > q_lo ? (q_hi - q_lo + kBQ - 1) / kBQ : 0;
+  const int ntot = ntile_q * grp;
+
+  const int qbytes = (int)(a.qss * 2), obytes = (int)(a.doss * 2);
+
+  const LaneOffs<D> lo = lane_offs<D>(lane);
+  Frag<T> kf[2][D / 32], vf[2][D / 32];
+  int qmin[2], qmax[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int row = kw + 16 * kb + l16;
+    // tile rows at or past q_hi are clamped copies of row q_hi - 1: excluded
+    if (GLOB) {
+      qmin[kb] = row < nrows ? glob_row_first_query(row, W, a.rpb) : S;
+      qmax[kb] = q_hi - 1;
+    } else {
+      qmin[kb] = row;
+      qmax[kb] = min(row + W, q_hi) - 1;
+    }
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      if (row < nrows) {
+        kf[kb][c] = lds_frag_row<T>(kbase + (int64_t)row * kstride + 32 * c + 8 * g);
+        vf[kb][c] = lds_frag_row<T>(vbase + (int64_t)row * vstride + 32 * c + 8 * g);
+      } else {
+        zero_frag(kf[kb][c]);
+        zero_frag(vf[kb][c]);
+      }
+    }
+  }
+  f32x4 dka[D / 16][2], dva[D / 16][2];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+    dka[db][0] = dka[db][1] = dva[db][0] = dva[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool active = kw < nrows;
+  const int k_last = min(kw + kKW, nrows) - 1;
+  // queries this wave can see at all
+  const int wq_lo = GLOB ? (active ? max(q_lo, glob_row_first_query(kw, W, a.rpb)) : S) : kw;
+  const int wq_hi = GLOB ? q_hi : min(q_hi, kw + kKW - 1 + W);
+  const int full_lo = GLOB ? (active ? glob_row_first_query(k_last, W, a.rpb) : S) : k_last;
+  const int full_hi = GLOB ? q_hi : kw + W;  // exclusive
+  const float c2 = a.scale * kLog2e;
+
+  // Tile `it` = query tile it % ntile_q of group head it / ntile_q; buffer
+  // resources are built per head (scalar work).
+  auto load_tile = [&](int it, int buf) {
+    const int j = it / ntile_q;
+    const int ts = q_lo + (it - j * ntile_q) * kBQ;
+    const int hq = hk * grp + j;
+    const int64_t bh = (int64_t)b * a.Hq + hq;
+    const __amdgpu_buffer_rsrc_t rq =
+        make_rsrc(static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh,
+                  (uint32_t)(((S - 1) * a.qss + D) * 2));
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(static_cast<const T*>(a.dout) + b * a.dosb + hq * a.dosh,
+                  (uint32_t)(((S - 1) * a.doss + D) * 2));
+    Tile::template load<4>(lds[buf][0], rq, qbytes, ts, 0, q_hi, wave, lane);
+    Tile::template load<4>(lds[buf][1], ro, obytes, ts, 0, q_hi, wave, lane);
+    if (wave == 0) {
+      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + bh * S, (uint32_t)(S * 4));
+      const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.delta + bh * S, (uint32_t)(S * 4));
+      const int qrow = min(ts + lane, q_hi - 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, CRA_LDS(&sLD[buf][0][0]), 4, qrow * 4, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, CRA_LDS(&sLD[buf][1][0]), 4, qrow * 4, 0, 0, 0);
+    }
+  };
+  if (ntot > 0) load_tile(0, 0);
+
+  auto step = [&](auto BUFC, int it) {
+    constexpr int BUF = decltype(BUFC)::value;
+    wait_vmem();
+    __syncthreads();
+    if (it + 1 < ntot) load_tile(it + 1, BUF ^ 1);
+    const int j = it / ntile_q;
+    const int ts = q_lo + (it - j * ntile_q) * kBQ;
+    const int t_last = min(ts + kBQ, q_hi) - 1;
+    if (active && t_last >= wq_lo && ts < wq_hi) {
+      const bool full = ts >= full_lo && ts + kBQ <= full_hi && ts + kBQ <= q_hi;
+      if (full)
+        dkdv2_tile<T, D, false>(lds[BUF][0], lds[BUF][1], sLD[BUF][0], sLD[BUF][1], lo, kf, vf,
+                                dka, dva, c2, g, ts, qmin, qmax);
+      else
+        dkdv2_tile<T, D, true>(lds[BUF][0], lds[BUF][1], sLD[BUF][0], sLD[BUF][1], lo, kf, vf,
+                               dka, dva, c2, g, ts, qmin, qmax);
+    }
+  };
+  for (int it = 0; it < ntot; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
+  }
+
+  if (GLOB) {
+    float* part = a.gpart + ((int64_t)chunk * nbh + bhk) * a.G * 2 * D;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int row = kw + 16 * kb + l16;
+      if (row >= nrows) continue;
+      float* pk = part + (int64_t)row * 2 * D;
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        *reinterpret_cast<f32x4*>(pk + 16 * db + 4 * g) = dka[db][kb] * a.scale;
+        *reinterpret_cast<f32x4*>(pk + D + 16 * db + 4 * g) = dva[db][kb];
+      }
+    }
+    return;
+  }
+  T* dkp = static_cast<T*>(a.dk) + b * a.dksb + hk * a.dksh;
+  T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh;
+  const float rsc = (a.relay && a.rscale) ? a.rscale[hk] : 1.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    const int j = kw + 16 * kb + l16;
+    if (j >= S) continue;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) dka[db][kb] *= a.scale;
+    const int rblk = j / W;
+    int grow[5];
+    float gsc[5];
+    int nm = 0;
+    if (j == rblk * W) {
+      grow[nm] = rblk * a.rpb;
+      gsc[nm++] = 1.f;
+    }
+    if (a.relay) {
+      const int32_t* src = a.src + ((int64_t)bhk * (a.G / a.rpb) + rblk) * a.top_k;
+      for (int t = 0; t < a.top_k; ++t) {
+        if (src[t] == j) {
+          grow[nm] = rblk * a.rpb + 1 + t;
+          gsc[nm++] = rsc;
+        }
+      }
+    }
+    for (int m = 0; m < nm; ++m) {
+      for (int c = 0; c < a.nchunk; ++c) {
+        const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + grow[m]) * 2 * D;
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) {
+          dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
+          dva[db][kb] += *reinterpret_cast<const f32x4*>(pk + D + 16 * db + 4 * g) * gsc[m];
+        }
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      store4<T>(dkp + (int64_t)j * a.dkss + 16 * db + 4 * g, dka[db][kb], 1.f);
+      store4<T>(dvp + (int64_t)j * a.dvss + 16 * db + 4 * g, dva[db][kb], 1.f);
+    }
+  }
+}
+
 template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   using Tr = BwdTraits<T, D>;
@@ -576,15 +1050,25 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq), dim3(256),
                      0, st, a);
   const int qtiles = (a.S + Tr::kBM - 1) / Tr::kBM;
-  hipLaunchKernelGGL((dq_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
   const int gtiles = (int)((a.G + Tr::kBK - 1) / Tr::kBK);
-  hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv), dim3(256),
-                     0, st, a, gtiles);
+  const int ktiles = (a.S + Tr::kBK - 1) / Tr::kBK;
+  if constexpr (sizeof(T) == 2) {
+    hipLaunchKernelGGL((dq2_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv),
+                       dim3(256), 0, st, a, gtiles);
+  } else {
+    hipLaunchKernelGGL((dq_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
+    hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv),
+                       dim3(256), 0, st, a, gtiles);
+  }
   if (a.dalpha && a.relay)
     hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
-  const int ktiles = (a.S + Tr::kBK - 1) / Tr::kBK;
-  hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st, a,
-                     ktiles);
+  if constexpr (sizeof(T) == 2)
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st,
+                       a, ktiles);
+  else
+    hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st,
+                       a, ktiles);
   return hipGetLastError();
 }
 

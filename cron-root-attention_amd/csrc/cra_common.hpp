@@ -191,4 +191,128 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// ---------------------------------------------------------------------------
+// gfx950 LDS tiles for 2-byte elements: ROWS x D, row-major, no padding,
+// 16-byte chunks XOR-swizzled per row so that 16 lanes reading the same
+// chunk of 16 consecutive rows hit 16 different bank groups.
+//
+// Filled straight from HBM with global_load_lds (16 B per lane; lane i of an
+// instruction lands at LDS base + 16 i, so each lane fetches the global chunk
+// that belongs at its LDS position). Read either as 16-byte row fragments or
+// transposed with ds_read_b64_tr_b16: in each 16-lane group, result lane L,
+// slot j receives element L%4 of what source lane 4j + L/4 addressed, so if
+// source lane 4j+m addresses row r_j, columns c0+4m .. c0+4m+3, result lane L
+// holds column c0+L of rows r_0..r_3 -- a transposed MFMA operand.
+// ---------------------------------------------------------------------------
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+#define CRA_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+template <int D, int ROWS>
+struct SwzTile {
+  static_assert(D == 32 || D == 64 || D == 128, "head dim");
+  static constexpr int kCPR = D / 8;      // 16-byte chunks per row
+  static constexpr int kRPL = 128 / D;    // rows sharing one 256-byte line
+  static constexpr int kBytes = ROWS * D * 2;
+  static constexpr int kInstr = ROWS * kCPR / 64;  // 1 KB global_load_lds per instruction
+
+  __device__ __forceinline__ static int swz(int row) { return (row / kRPL) % kCPR; }
+  // byte offset of logical 16-byte chunk `chunk` of `row`
+  __device__ __forceinline__ static int off(int row, int chunk) {
+    return row * (D * 2) + ((chunk ^ swz(row)) << 4);
+  }
+
+  // Cooperative fill by NWAVES waves from a buffer resource whose rows are
+  // row_bytes apart: tile row i <- global row clamp(row0 + i, row_lo,
+  // row_hi - 1). Rows outside [row_lo, row_hi) hold a copy of an edge row;
+  // callers mask them. Each lane needs one 32-bit offset per instruction.
+  template <int NWAVES>
+  __device__ __forceinline__ static void load(char* lds, __amdgpu_buffer_rsrc_t rsrc,
+                                              int row_bytes, int row0, int row_lo, int row_hi,
+                                              int wave, int lane) {
+    static_assert(kInstr % NWAVES == 0, "instructions per wave");
+    constexpr int kPer = kInstr / NWAVES;
+#pragma unroll
+    for (int t0 = 0; t0 < kPer; ++t0) {
+      const int t = wave * kPer + t0;
+      const int idx = t * 64 + lane;
+      const int row = idx / kCPR;
+      const int chunk = (idx % kCPR) ^ swz(row);
+      const int grow = min(max(row0 + row, row_lo), row_hi - 1);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, CRA_LDS(lds + t * 1024), 16,
+                                               grow * row_bytes + chunk * 16, 0, 0, 0);
+    }
+  }
+
+  // 8 consecutive elements (16 B) of `row` starting at column 8*chunk.
+  template <typename T>
+  __device__ __forceinline__ static Frag<T> row_frag(const char* lds, int row, int chunk) {
+    Frag<T> f;
+    f.w[0] = *reinterpret_cast<const uint4*>(lds + off(row, chunk));
+    return f;
+  }
+
+  // The swizzle repeats every 16 rows (16 / kRPL is a multiple of kCPR), so
+  // for rows 16*blk + r the offset is blk * 16 * row_bytes + lane_off(r, ..):
+  // lane-constant parts are computed once and the block term folds into the
+  // instruction's immediate offset.
+  static constexpr int kBlk16 = 16 * D * 2;
+  // row fragment of row 16*blk + (lane%16), chunk `chunk`
+  __device__ __forceinline__ static int row_lane_off(int lane, int chunk) {
+    return off(lane & 15, chunk);
+  }
+  // transposed fragment at column c0: rows 16*blk + 4g + j, this lane's part
+  __device__ __forceinline__ static int tr_lane_off(int lane, int c0) {
+    const int L = lane & 15, g = lane >> 4;
+    const int col = c0 + 4 * (L & 3);
+    return off(4 * g + (L >> 2), col >> 3) + ((col & 7) << 1);
+  }
+  template <typename T>
+  __device__ __forceinline__ static Frag<T> row_frag_at(const char* p) {
+    Frag<T> f;
+    f.w[0] = *reinterpret_cast<const uint4*>(p);
+    return f;
+  }
+  // pa: rows 16*blk_a + ..; pb: rows 16*blk_b + .. (both already offset)
+  template <typename T>
+  __device__ __forceinline__ static Frag<T> tr_frag_at(const char* pa, const char* pb) {
+    i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)pa);
+    i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)pb);
+    Frag<T> f;
+    const uint2 ux = __builtin_bit_cast(uint2, x);
+    const uint2 uy = __builtin_bit_cast(uint2, y);
+    f.w[0] = make_uint4(ux.x, ux.y, uy.x, uy.y);
+    return f;
+  }
+
+  // Transposed operand: lane (L = lane%16, g = lane/16) gets column c0 + L of
+  // rows ra + 4g + j (slots 0..3) and rb + 4g + j (slots 4..7).
+  template <typename T>
+  __device__ __forceinline__ static Frag<T> tr_frag(const char* lds, int ra, int rb, int c0,
+                                                    int lane) {
+    const int L = lane & 15, g = lane >> 4;
+    const int j = L >> 2, m = L & 3;
+    const int col = c0 + 4 * m;
+    const int ca = ra + 4 * g + j, cb = rb + 4 * g + j;
+    const int oa = off(ca, col >> 3) + ((col & 7) << 1);
+    const int ob = off(cb, col >> 3) + ((col & 7) << 1);
+    i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(lds + oa));
+    i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(lds + ob));
+    Frag<T> f;
+    const uint2 ux = __builtin_bit_cast(uint2, x);
+    const uint2 uy = __builtin_bit_cast(uint2, y);
+    f.w[0] = make_uint4(ux.x, ux.y, uy.x, uy.y);
+    return f;
+  }
+};
+
+// Wait until this wave's outstanding global loads (incl. loads to LDS) landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
 }  // namespace cra

@@ -19,6 +19,8 @@
 // straight from the S^T registers. Tiles are launched heaviest first (work
 // per query grows with i) and consecutive workgroups are different heads of
 // the same tile, so each XCD keeps a fixed pair of heads.
+#include <type_traits>
+
 #include "cra_common.hpp"
 #include "cra_internal.hpp"
 
@@ -237,14 +239,245 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16/bf16 forward. Same mapping as fwd_kernel (4 waves x 32 queries), but
+// K/V tiles (64 rows) are double-buffered in swizzled LDS, filled with
+// global_load_lds while the previous tile is computed, V^T operands come from
+// ds_read_b64_tr_b16 on the row-major V tile, each tile is processed in two
+// 32-key halves, and the running max is raised only when a score exceeds it
+// by more than 2^8 (P stays <= 256; O and LSE are exact for any reference max).
+// ---------------------------------------------------------------------------
+template <int D>
+struct Fwd2Lane {
+  int k[D / 32];   // K row fragment, chunk 4c + g, row lane%16
+  int v[D / 16];   // V^T fragment, columns 16 db ..
+};
+
+template <typename T, int D, bool MASK, typename Valid>
+__device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, const Fwd2Lane<D>& lo,
+                                             const Frag<T> (&qf)[2][D / 32],
+                                             f32x4 (&acc)[D / 16][2], float (&m_run)[2],
+                                             float (&l_run)[2], float c2, int g, Valid valid) {
+  using Tile = SwzTile<D, 64>;
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc) {
+    f32x4 s[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kb = 2 * kc + h;
+      s[h][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[h][1] = s[h][0];
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.k[c]);
+        s[h][0] = mma(s[h][0], kf, qf[0][c]);
+        s[h][1] = mma(s[h][1], kf, qf[1][c]);
+      }
+    }
+    Frag<T> pf[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = -__builtin_huge_valf();
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (MASK && !valid(32 * kc + 16 * h + 4 * g + r, qb)) s[h][qb][r] = -__builtin_huge_valf();
+          mx = fmaxf(mx, s[h][qb][r]);
+        }
+      const float ml = mx * c2;
+      const bool need = m_run[qb] == -__builtin_huge_valf() ? ml > m_run[qb]
+                                                            : ml > m_run[qb] + 8.f;
+      if (__any(need)) {
+        const float mt = group_max(ml);
+        const float m_new = fmaxf(m_run[qb], mt);
+        const float alpha = m_run[qb] == -__builtin_huge_valf()
+                                ? 0.f
+                                : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
+        m_run[qb] = m_new;
+      }
+      const float mu = m_run[qb] == -__builtin_huge_valf() ? 0.f : m_run[qb];
+      float pv[8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -mu));
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ps += pv[i];
+      l_run[qb] += ps;
+      pf[qb] = pack8<T>(pv);
+    }
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      const char* pa = tV + (2 * kc) * Tile::kBlk16 + lo.v[db];
+      const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+      acc[db][0] = mma(acc[db][0], vt, pf[0]);
+      acc[db][1] = mma(acc[db][1], vt, pf[1]);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void fwd2_kernel(FwdArgs a) {
+  using Tile = SwzTile<D, 64>;
+  constexpr int kBM = 128, kQW = 32, kBN = 64;
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int nbh = a.B * a.Hq;
+  const int bh = blockIdx.x % nbh;
+  const int tile = a.ntiles - 1 - (int)(blockIdx.x / nbh);
+  const int b = bh / a.Hq, h = bh % a.Hq;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int m0 = tile * kBM;
+  const int q0 = m0 + wave * kQW;
+  const int S = a.S, W = a.W;
+
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* gkp = static_cast<const T*>(a.gk) + gbase;
+  const T* gvp = static_cast<const T*>(a.gv) + gbase;
+
+  const int lo_k = max(0, m0 - W + 1);
+  const int hi = min(S, m0 + kBM);
+  const int gmax = glob_prefix(hi - 1, W, a.rpb);
+  const int nloc = (hi - lo_k + kBN - 1) / kBN;
+  const int ntot = nloc + (gmax + kBN - 1) / kBN;
+
+  // Buffer resources over this (b, h)'s rows: 32-bit offsets, uniform bases.
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((S - 1) * a.kss * 2 + D * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((S - 1) * a.vss * 2 + D * 2));
+  const __amdgpu_buffer_rsrc_t rgk = make_rsrc(gkp, (uint32_t)(a.G * D * 2));
+  const __amdgpu_buffer_rsrc_t rgv = make_rsrc(gvp, (uint32_t)(a.G * D * 2));
+  const int kbytes = (int)(a.kss * 2), vbytes = (int)(a.vss * 2);
+  auto issue = [&](int it, char* dst) {
+    if (it < nloc) {
+      const int ts = lo_k + it * kBN;
+      Tile::template load<4>(dst, rk, kbytes, ts, 0, hi, wave, lane);
+      Tile::template load<4>(dst + Tile::kBytes, rv, vbytes, ts, 0, hi, wave, lane);
+    } else {
+      const int ts = (it - nloc) * kBN;
+      Tile::template load<4>(dst, rgk, D * 2, ts, 0, gmax, wave, lane);
+      Tile::template load<4>(dst + Tile::kBytes, rgv, D * 2, ts, 0, gmax, wave, lane);
+    }
+  };
+  issue(0, lds[0][0]);
+
+  Fwd2Lane<D> lo;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) lo.k[c] = Tile::row_lane_off(lane, 4 * c + g);
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) lo.v[db] = Tile::tr_lane_off(lane, 16 * db);
+
+  Frag<T> qf[2][D / 32];
+  int qi[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    qi[qb] = q0 + 16 * qb + l16;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      if (qi[qb] < S)
+        qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qi[qb] * a.qss + 32 * c + 8 * g);
+      else
+        qf[qb][c].w[0] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  const float c2 = a.scale * kLog2e;
+  float m_run[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
+  float l_run[2] = {0.f, 0.f};
+  f32x4 acc[D / 16][2];
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db][0] = acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const bool active = q0 < S;
+  const int q_last = min(q0 + kQW, S) - 1;
+  const int w_lo = max(0, q0 - W + 1);
+  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+
+  // One pipeline step on buffer BUF: wait for its tile, start the next one in
+  // the other buffer, compute.
+  auto step = [&](auto BUFC, int it) {
+    constexpr int BUF = decltype(BUFC)::value;
+    wait_vmem();
+    __syncthreads();
+    if (it + 1 < ntot) issue(it + 1, lds[BUF ^ 1][0]);
+    const char* tK = lds[BUF][0];
+    const char* tV = lds[BUF][1];
+    if (it < nloc) {
+      const int ts = lo_k + it * kBN;
+      if (active && ts <= q_last && ts + kBN - 1 >= w_lo) {
+        auto valid = [&](int ko, int qb) {
+          const int j = ts + ko;
+          return j <= qi[qb] && j >= qi[qb] - W + 1;
+        };
+        if (ts >= q_last - W + 1 && ts + kBN - 1 <= q0)
+          attend_tile2<T, D, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
+        else
+          attend_tile2<T, D, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
+      }
+    } else {
+      const int ts = (it - nloc) * kBN;
+      if (active && ts < wg_hi) {
+        auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
+        if (ts + kBN <= wg_lo)
+          attend_tile2<T, D, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
+        else
+          attend_tile2<T, D, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
+      }
+    }
+  };
+  for (int it = 0; it < ntot; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
+  }
+
+  T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l = group_sum(l_run[qb]);
+    if (!active || qi[qb] >= S) continue;
+    const float inv = 1.f / fmaxf(l, 1e-6f);
+    T* orow = op + (int64_t)qi[qb] * a.oss;
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      T e[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) e[r] = from_f32<T>(acc[db][qb][r] * inv);
+      *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = *reinterpret_cast<const uint2*>(e);
+    }
+    if (g == 0)
+      a.lse[(int64_t)bh * S + qi[qb]] = (m_run[qb] + __builtin_amdgcn_logf(fmaxf(l, 1e-6f))) * kLn2;
+  }
+}
+
 template <typename T>
 hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
   dim3 grid(a.ntiles * a.B * a.Hq);
-  switch (D) {
-    case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
-    case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
-    case 128: hipLaunchKernelGGL((fwd_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
-    default: return hipErrorInvalidValue;
+  if constexpr (sizeof(T) == 2) {
+    switch (D) {
+      case 32: hipLaunchKernelGGL((fwd2_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
+      case 64: hipLaunchKernelGGL((fwd2_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
+      case 128: hipLaunchKernelGGL((fwd2_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (D) {
+      case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
+      case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
+      case 128: hipLaunchKernelGGL((fwd_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   return hipGetLastError();
 }

@@ -239,12 +239,15 @@ def relay_select(k: torch.Tensor, plan: Plan, norm: str = "lanetree") -> torch.T
 
 def forward(q, k, v, plan: Plan, kv_groups: int = 1, src: Optional[torch.Tensor] = None,
             relay_scale: Optional[torch.Tensor] = None, chunk: int = 256,
-            norm: str = "lanetree", rows: Optional[tuple] = None):
+            norm: str = "lanetree", rows: Optional[tuple] = None,
+            relay_dtype: Optional[torch.dtype] = None):
     """Exact softmax over each query's multiset, fp64, differentiable.
 
     q: [B, Hq, S, D]; k, v: [B, Hkv, S, D]; query head h reads kv head
     h // kv_groups (core.py:981).  ``relay_scale`` ([Hkv], already
-    exponentiated) multiplies relay k and v rows (core.py:3541-3544).
+    exponentiated) multiplies relay k and v rows (core.py:3541-3544); with
+    ``relay_dtype`` the scaled rows are rounded to that dtype, as the
+    reference's in-dtype multiply does (the rounding is not differentiated).
     ``rows=(lo, hi)`` computes only queries [lo, hi) (outputs then hold those
     rows) so long sequences can be spot-checked.
     Returns (o [B,Hq,S,D] fp64, lse [B,Hq,S] fp64, src).
@@ -277,6 +280,9 @@ def forward(q, k, v, plan: Plan, kv_groups: int = 1, src: Optional[torch.Tensor]
             sc = relay_scale.to(torch.float64)[kv_idx].view(1, Hq, 1, 1)
             Kr = Kr * sc
             Vr = Vr * sc
+            if relay_dtype is not None and relay_dtype != torch.float64:
+                Kr = Kr + (Kr.detach().to(relay_dtype).to(torch.float64) - Kr.detach())
+                Vr = Vr + (Vr.detach().to(relay_dtype).to(torch.float64) - Vr.detach())
         r_end = (torch.arange(NB * plan.top_k) // plan.top_k + 1) * W - 1
     outs, lses = [], []
     lo, hi = (0, S) if rows is None else rows

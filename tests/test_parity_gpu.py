@@ -175,7 +175,7 @@ def test_forward_strided_views_and_relay_scale():
     o = cra.cron_root_attention(xd[:, :, 0].transpose(1, 2), xd[:, :, 1].transpose(1, 2),
                                 xd[:, :, 2].transpose(1, 2), relay_log_scale=alpha.to(DEV))
     rs = alpha.exp().to(F16).to(F32)
-    check_forward(o, q, k, v, plan_for(S), F16, relay_scale=rs)
+    check_forward(o, q, k, v, plan_for(S), F16, relay_scale=rs, relay_dtype=F16)
 
 
 @pytest.mark.parametrize("shape", SHAPES)
