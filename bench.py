@@ -70,6 +70,23 @@ def timed(fn, steps, warmup, torch):
     return e0.elapsed_time(e1) / steps
 
 
+def per_launch_ms(fn, steps, warmup, torch):
+    """Average duration of single launches, each bracketed by its own pair of
+    events on the current stream (the stream the library launches on), so
+    that no launch overlaps the next one's start, as in a kernel trace."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+
+
 def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
     """Oracle CPU port (fp32 forward) on the host cores: pairs of heads of the
     same workload, each over all S queries, until ~budget_s of CPU time (or
@@ -132,7 +149,8 @@ def run_main(args):
     W = int(math.ceil(math.sqrt(S)))
     p = _native.problem(B, H, H, S, D, W, True, 2, dtype, 1 / math.sqrt(D))
     gk, gv, _ = _native.build_global(p, k, v, None)
-    kern_ms = timed(lambda: _native.forward(p, q, k, v, gk, gv), args.steps, args.warmup, torch)
+    kern_ms = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv), args.steps, args.warmup,
+                            torch)
     achieved = f_fwd / (kern_ms * 1e-3) / 1e12
     workload = "H16_D128_S131072_fp16"
     roof = {"kernel": "fwd2_kernel<f16,128>", "bound": "mfma", "achieved": round(achieved, 2),
@@ -157,6 +175,34 @@ def run_main(args):
         "pairs_per_head": P, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def run_profile_workload(args):
+    """Short fixed workload for counter passes (rocprofv3 --pmc): a 1 GiB
+    device copy first (read 1 GiB + write 1 GiB, the calibration of
+    FETCH_SIZE / WRITE_SIZE), then the hot path's kernels: build_global and
+    cra_fwd twice each, then one backward."""
+    import torch
+    from cron_root_attention import _native
+    dev = torch.device("cuda", 0)
+    x = torch.empty(512 * 1024 * 1024, dtype=torch.float16, device=dev).fill_(1.0)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    B, H, S, D = 1, 16, 131072, 128
+    gen = torch.Generator(device=dev).manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=gen, device=dev, dtype=torch.float32).half()
+                   for _ in range(4))
+    W = int(math.ceil(math.sqrt(S)))
+    p = _native.problem(B, H, H, S, D, W, True, 2, torch.float16, 1 / math.sqrt(D))
+    for _ in range(2):
+        gk, gv, src = _native.build_global(p, k, v, None)
+        o, lse = _native.forward(p, q, k, v, gk, gv)
+    _native.backward(p, q, k, v, o, do, lse, gk, gv, src, None, False)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_workload": "done", "B": B, "H": H, "S": S, "D": D}), flush=True)
 
 
 def run_crossover(args):
@@ -194,6 +240,8 @@ def main(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--crossover", action="store_true")
+    ap.add_argument("--profile-workload", action="store_true",
+                    help="copy calibration + hot-path kernels once, for counter passes")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -201,6 +249,8 @@ def main(argv=None):
         return 2
     if args.crossover:
         run_crossover(args)
+    elif args.profile_workload:
+        run_profile_workload(args)
     else:
         run_main(args)
     return 0

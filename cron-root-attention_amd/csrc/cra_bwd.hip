@@ -596,12 +596,12 @@ __device__ __forceinline__ LaneOffs<D> lane_offs(int lane) {
   return o;
 }
 
-template <typename T, int D, bool MASK, typename Valid>
+template <typename T, int D, bool MASK>
 __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const LaneOffs<D>& lo,
                                          const Frag<T> (&qf)[2][D / 32],
                                          const Frag<T> (&df)[2][D / 32], f32x4 (&dqa)[D / 16][2],
                                          const float (&lse2)[2], const float (&dl)[2], float c2,
-                                         int g, Valid valid) {
+                                         int g, const TileMask& mk) {
   using Tile = SwzTile<D, 64>;
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
@@ -625,8 +625,8 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
         float x0 = fmaf(s0[r], c2, -lse2[0]);
         float x1 = fmaf(s1[r], c2, -lse2[1]);
         if (MASK) {
-          if (!valid(ko, 0)) x0 = -__builtin_huge_valf();
-          if (!valid(ko, 1)) x1 = -__builtin_huge_valf();
+          if (!mk.ok(ko, 0)) x0 = -__builtin_huge_valf();
+          if (!mk.ok(ko, 1)) x1 = -__builtin_huge_valf();
         }
         ds[h][0][r] = __builtin_amdgcn_exp2f(x0) * (p0[r] - dl[0]);
         ds[h][1][r] = __builtin_amdgcn_exp2f(x1) * (p1[r] - dl[1]);
@@ -649,8 +649,11 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
   }
 }
 
+// At least 2 waves per SIMD: the loop body is a single copy of the tile code,
+// which leaves the D = 128 kernel 246 VGPRs and no spills.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void dq2_kernel(BwdArgs a, int ntiles) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void dq2_kernel(BwdArgs a, int ntiles) {
   using Tile = SwzTile<D, 64>;
   constexpr int kBM = 128, kQW = 32, kBN = 64;
   __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
@@ -731,39 +734,31 @@ __global__ __launch_bounds__(256) void dq2_kernel(BwdArgs a, int ntiles) {
   const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
   const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
 
-  auto step = [&](auto BUFC, int it) {
-    constexpr int BUF = decltype(BUFC)::value;
+  // One loop body for local and global tiles (parameters chosen per tile),
+  // so the accumulators stay in place across iterations.
+  for (int it = 0; it < ntot; ++it) {
+    const int buf = it & 1;
     wait_vmem();
     __syncthreads();
-    if (it + 1 < ntot) issue(it + 1, lds[BUF ^ 1][0]);
-    const char* tK = lds[BUF][0];
-    const char* tV = lds[BUF][1];
-    if (it < nloc) {
-      const int ts = lo_k + it * kBN;
-      if (active && ts <= q_last && ts + kBN - 1 >= w_lo) {
-        auto valid = [&](int ko, int qb) {
-          const int j = ts + ko;
-          return j <= qi[qb] && j >= qi[qb] - W + 1;
-        };
-        if (ts >= q_last - W + 1 && ts + kBN - 1 <= q0)
-          dq2_tile<T, D, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
-        else
-          dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
-      }
-    } else {
-      const int ts = (it - nloc) * kBN;
-      if (active && ts < wg_hi) {
-        auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
-        if (ts + kBN <= wg_lo)
-          dq2_tile<T, D, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
-        else
-          dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, valid);
-      }
+    if (it + 1 < ntot) issue(it + 1, lds[buf ^ 1][0]);
+    const char* tK = lds[buf][0];
+    const char* tV = lds[buf][1];
+    const bool loc = it < nloc;
+    const int ts = loc ? lo_k + it * kBN : (it - nloc) * kBN;
+    const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
+    const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
+    TileMask mk;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      mk.hi[qb] = loc ? qi[qb] - ts : glen[qb] - 1 - ts;
+      mk.span[qb] = loc ? (unsigned)(W - 1) : 0x7fffffffu;
     }
-  };
-  for (int it = 0; it < ntot; it += 2) {
-    step(std::integral_constant<int, 0>{}, it);
-    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
+    if (work) {
+      if (full)
+        dq2_tile<T, D, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
+      else
+        dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
+    }
   }
 
   T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;

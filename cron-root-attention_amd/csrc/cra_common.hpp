@@ -65,13 +65,25 @@ __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <typename T>
 __device__ __forceinline__ float to_f32(T x) { return (float)x; }
 
-// Packs eight fp32 values into a fragment of T.
+// Packs eight fp32 values into a fragment of T (pairwise conversions, round
+// to nearest even).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
 template <typename T>
 __device__ __forceinline__ Frag<T> pack8(const float (&v)[8]) {
   Frag<T> f;
-  T* e = reinterpret_cast<T*>(f.w);
+  if constexpr (sizeof(T) == 2) {
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    uint32_t* w = reinterpret_cast<uint32_t*>(f.w);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) e[s] = from_f32<T>(v[s]);
+    for (int s = 0; s < 4; ++s)
+      w[s] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v[2 * s], v[2 * s + 1]}, t2));
+  } else {
+    T* e = reinterpret_cast<T*>(f.w);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) e[s] = from_f32<T>(v[s]);
+  }
   return f;
 }
 
@@ -229,11 +241,11 @@ struct SwzTile {
   __device__ __forceinline__ static void load(char* lds, __amdgpu_buffer_rsrc_t rsrc,
                                               int row_bytes, int row0, int row_lo, int row_hi,
                                               int wave, int lane) {
-    static_assert(kInstr % NWAVES == 0, "instructions per wave");
-    constexpr int kPer = kInstr / NWAVES;
+    constexpr int kPer = (kInstr + NWAVES - 1) / NWAVES;
 #pragma unroll
     for (int t0 = 0; t0 < kPer; ++t0) {
-      const int t = wave * kPer + t0;
+      const int t = t0 * NWAVES + wave;
+      if (kInstr % NWAVES != 0 && t >= kInstr) break;
       const int idx = t * 64 + lane;
       const int row = idx / kCPR;
       const int chunk = (idx % kCPR) ^ swz(row);
@@ -308,6 +320,18 @@ struct SwzTile {
 };
 
 // Wait until this wave's outstanding global loads (incl. loads to LDS) landed.
+// Mask of one tile for one query block: key row `ts + ko` is visible to the
+// lane's query iff (unsigned)(hi - ko) <= span. Local window: hi = qi - ts,
+// span = W - 1 (qi - W + 1 <= ts + ko <= qi); global prefix: hi = glen - 1 - ts,
+// span = 2^31 - 1 (ts + ko < glen).
+struct TileMask {
+  int hi[2];
+  unsigned span[2];
+  __device__ __forceinline__ bool ok(int ko, int qb) const {
+    return (unsigned)(hi[qb] - ko) <= span[qb];
+  }
+};
+
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3).

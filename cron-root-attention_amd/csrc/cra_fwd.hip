@@ -253,14 +253,15 @@ struct Fwd2Lane {
   int v[D / 16];   // V^T fragment, columns 16 db ..
 };
 
-template <typename T, int D, bool MASK, typename Valid>
+template <typename T, int D, int BN, bool MASK>
 __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, const Fwd2Lane<D>& lo,
                                              const Frag<T> (&qf)[2][D / 32],
                                              f32x4 (&acc)[D / 16][2], float (&m_run)[2],
-                                             float (&l_run)[2], float c2, int g, Valid valid) {
-  using Tile = SwzTile<D, 64>;
+                                             float (&l_run)[2], float c2, int g,
+                                             const TileMask& mk) {
+  using Tile = SwzTile<D, BN>;
 #pragma unroll
-  for (int kc = 0; kc < 2; ++kc) {
+  for (int kc = 0; kc < BN / 32; ++kc) {
     f32x4 s[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -282,7 +283,7 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if (MASK && !valid(32 * kc + 16 * h + 4 * g + r, qb)) s[h][qb][r] = -__builtin_huge_valf();
+          if (MASK && !mk.ok(32 * kc + 16 * h + 4 * g + r, qb)) s[h][qb][r] = -__builtin_huge_valf();
           mx = fmaxf(mx, s[h][qb][r]);
         }
       const float ml = mx * c2;
@@ -305,10 +306,7 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -mu));
-      float ps = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ps += pv[i];
-      l_run[qb] += ps;
+      l_run[qb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
       pf[qb] = pack8<T>(pv);
     }
 #pragma unroll
@@ -321,11 +319,13 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// BN: key rows per LDS tile (64: 2 x 32 KB double buffer, 2 waves/SIMD;
+// 32: 2 x 16 KB, 3 waves/SIMD).
+template <typename T, int D, int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN == 64 ? 2 : 3, BN == 64 ? 2 : 3)))
 void fwd2_kernel(FwdArgs a) {
-  using Tile = SwzTile<D, 64>;
-  constexpr int kBM = 128, kQW = 32, kBN = 64;
+  using Tile = SwzTile<D, BN>;
+  constexpr int kBM = 128, kQW = 32, kBN = BN;
   __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
 
   const int tid = threadIdx.x;
@@ -405,41 +405,31 @@ void fwd2_kernel(FwdArgs a) {
   const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
   const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
 
-  // One pipeline step on buffer BUF: wait for its tile, start the next one in
-  // the other buffer, compute.
-  auto step = [&](auto BUFC, int it) {
-    constexpr int BUF = decltype(BUFC)::value;
+  // One loop body for local and global tiles (parameters chosen per tile),
+  // so the accumulators stay in place across iterations.
+  for (int it = 0; it < ntot; ++it) {
+    const int buf = it & 1;
     wait_vmem();
     __syncthreads();
-    if (it + 1 < ntot) issue(it + 1, lds[BUF ^ 1][0]);
-    const char* tK = lds[BUF][0];
-    const char* tV = lds[BUF][1];
-    if (it < nloc) {
-      const int ts = lo_k + it * kBN;
-      if (active && ts <= q_last && ts + kBN - 1 >= w_lo) {
-        auto valid = [&](int ko, int qb) {
-          const int j = ts + ko;
-          return j <= qi[qb] && j >= qi[qb] - W + 1;
-        };
-        if (ts >= q_last - W + 1 && ts + kBN - 1 <= q0)
-          attend_tile2<T, D, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
-        else
-          attend_tile2<T, D, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
-      }
-    } else {
-      const int ts = (it - nloc) * kBN;
-      if (active && ts < wg_hi) {
-        auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
-        if (ts + kBN <= wg_lo)
-          attend_tile2<T, D, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
-        else
-          attend_tile2<T, D, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, valid);
-      }
+    if (it + 1 < ntot) issue(it + 1, lds[buf ^ 1][0]);
+    const char* tK = lds[buf][0];
+    const char* tV = lds[buf][1];
+    const bool loc = it < nloc;
+    const int ts = loc ? lo_k + it * kBN : (it - nloc) * kBN;
+    const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
+    const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
+    TileMask mk;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      mk.hi[qb] = loc ? qi[qb] - ts : glen[qb] - 1 - ts;
+      mk.span[qb] = loc ? (unsigned)(W - 1) : 0x7fffffffu;
     }
-  };
-  for (int it = 0; it < ntot; it += 2) {
-    step(std::integral_constant<int, 0>{}, it);
-    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
+    if (work) {
+      if (full)
+        attend_tile2<T, D, BN, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
+      else
+        attend_tile2<T, D, BN, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
+    }
   }
 
   T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
@@ -465,10 +455,13 @@ template <typename T>
 hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
   dim3 grid(a.ntiles * a.B * a.Hq);
   if constexpr (sizeof(T) == 2) {
+#ifndef CRA_FWD_BN
+#define CRA_FWD_BN 64
+#endif
     switch (D) {
-      case 32: hipLaunchKernelGGL((fwd2_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
-      case 64: hipLaunchKernelGGL((fwd2_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
-      case 128: hipLaunchKernelGGL((fwd2_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+      case 32: hipLaunchKernelGGL((fwd2_kernel<T, 32, CRA_FWD_BN>), grid, dim3(256), 0, st, a); break;
+      case 64: hipLaunchKernelGGL((fwd2_kernel<T, 64, CRA_FWD_BN>), grid, dim3(256), 0, st, a); break;
+      case 128: hipLaunchKernelGGL((fwd2_kernel<T, 128, CRA_FWD_BN>), grid, dim3(256), 0, st, a); break;
       default: return hipErrorInvalidValue;
     }
   } else {
