@@ -656,7 +656,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void dq2_kernel(BwdArgs a, int ntiles) {
   using Tile = SwzTile<D, 64>;
   constexpr int kBM = 128, kQW = 32, kBN = 64;
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
+  // Two pipeline stages as separate LDS objects (see fwd2_kernel).
+  __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];  // K, V
+  __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -683,23 +685,29 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   const int gmax = glob_prefix(hi - 1, W, a.rpb);
   const int nloc = (hi - lo_k + kBN - 1) / kBN;
   const int ntot = nloc + (gmax + kBN - 1) / kBN;
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((S - 1) * a.kss * 2 + D * 2));
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((S - 1) * a.vss * 2 + D * 2));
-  const __amdgpu_buffer_rsrc_t rgk = make_rsrc(gkp, (uint32_t)(a.G * D * 2));
-  const __amdgpu_buffer_rsrc_t rgv = make_rsrc(gvp, (uint32_t)(a.G * D * 2));
+  // Buffer resources over the rows this workgroup may read (local rows below
+  // hi, global rows below gmax): loads past them return zeros.
+  using Fill = typename Tile::template Fill<4>;
   const int kbytes = (int)(a.kss * 2), vbytes = (int)(a.vss * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((hi - 1) * kbytes + D * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((hi - 1) * vbytes + D * 2));
+  const __amdgpu_buffer_rsrc_t rgk = make_rsrc(gkp, (uint32_t)(gmax * D * 2));
+  const __amdgpu_buffer_rsrc_t rgv = make_rsrc(gvp, (uint32_t)(gmax * D * 2));
+  const int fk = Fill::lane_off(wave, lane, kbytes);
+  const int fv = Fill::lane_off(wave, lane, vbytes);
+  const int fg = Fill::lane_off(wave, lane, D * 2);
   auto issue = [&](int it, char* dst) {
     if (it < nloc) {
       const int ts = lo_k + it * kBN;
-      Tile::template load<4>(dst, rk, kbytes, ts, 0, hi, wave, lane);
-      Tile::template load<4>(dst + Tile::kBytes, rv, vbytes, ts, 0, hi, wave, lane);
+      Fill::load(dst, rk, fk, kbytes, ts, wave);
+      Fill::load(dst + Tile::kBytes, rv, fv, vbytes, ts, wave);
     } else {
       const int ts = (it - nloc) * kBN;
-      Tile::template load<4>(dst, rgk, D * 2, ts, 0, gmax, wave, lane);
-      Tile::template load<4>(dst + Tile::kBytes, rgv, D * 2, ts, 0, gmax, wave, lane);
+      Fill::load(dst, rgk, fg, D * 2, ts, wave);
+      Fill::load(dst + Tile::kBytes, rgv, fg, D * 2, ts, wave);
     }
   };
-  issue(0, lds[0][0]);
+  issue(0, stage0[0]);
 
   const LaneOffs<D> lo = lane_offs<D>(lane);
   Frag<T> qf[2][D / 32], df[2][D / 32];
@@ -734,15 +742,17 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
   const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
 
-  // One loop body for local and global tiles (parameters chosen per tile),
-  // so the accumulators stay in place across iterations.
-  for (int it = 0; it < ntot; ++it) {
-    const int buf = it & 1;
+  // Local and global tiles share one body (parameters chosen per tile); the
+  // loop is unrolled over the two stages.
+  auto step = [&](auto stage_c, int it) {
+    constexpr int kStage = decltype(stage_c)::value;
+    char(&cur)[2][Tile::kBytes] = kStage ? stage1 : stage0;
+    char(&nxt)[2][Tile::kBytes] = kStage ? stage0 : stage1;
     wait_vmem();
     __syncthreads();
-    if (it + 1 < ntot) issue(it + 1, lds[buf ^ 1][0]);
-    const char* tK = lds[buf][0];
-    const char* tV = lds[buf][1];
+    if (it + 1 < ntot) issue(it + 1, nxt[0]);
+    const char* tK = cur[0];
+    const char* tV = cur[1];
     const bool loc = it < nloc;
     const int ts = loc ? lo_k + it * kBN : (it - nloc) * kBN;
     const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
@@ -759,6 +769,10 @@ void dq2_kernel(BwdArgs a, int ntiles) {
       else
         dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
     }
+  };
+  for (int it = 0; it < ntot; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
   }
 
   T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;
@@ -843,8 +857,12 @@ template <typename T, int D, bool GLOB>
 __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
   using Tile = SwzTile<D, 64>;
   constexpr int kBK = 128, kKW = 32, kBQ = 64;
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
-  __shared__ __attribute__((aligned(16))) float sLD[2][2][kBQ];  // [buf][lse2, delta][q]
+  // Two pipeline stages as separate LDS objects (see fwd2_kernel): Q and dO
+  // rows, and their LSE and Delta.
+  __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];
+  __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
+  __shared__ __attribute__((aligned(16))) float sld0[2][kBQ];  // [lse, delta][q]
+  __shared__ __attribute__((aligned(16))) float sld1[2][kBQ];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -891,6 +909,9 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
   const int ntot = ntile_q * grp;
 
   const int qbytes = (int)(a.qss * 2), obytes = (int)(a.doss * 2);
+  using Fill = typename Tile::template Fill<4>;
+  const int fq = Fill::lane_off(wave, lane, qbytes);
+  const int fo = Fill::lane_off(wave, lane, obytes);
 
   const LaneOffs<D> lo = lane_offs<D>(lane);
   Frag<T> kf[2][D / 32], vf[2][D / 32];
@@ -933,45 +954,53 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
 
   // Tile `it` = query tile it % ntile_q of group head it / ntile_q; buffer
   // resources are built per head (scalar work).
-  auto load_tile = [&](int it, int buf) {
+  auto load_tile = [&](int it, char (&dst)[2][Tile::kBytes], float (&dsl)[2][kBQ]) {
     const int j = it / ntile_q;
     const int ts = q_lo + (it - j * ntile_q) * kBQ;
     const int hq = hk * grp + j;
     const int64_t bh = (int64_t)b * a.Hq + hq;
+    // rows at or past q_hi load as zeros
     const __amdgpu_buffer_rsrc_t rq =
         make_rsrc(static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh,
-                  (uint32_t)(((S - 1) * a.qss + D) * 2));
+                  (uint32_t)((q_hi - 1) * qbytes + D * 2));
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(static_cast<const T*>(a.dout) + b * a.dosb + hq * a.dosh,
-                  (uint32_t)(((S - 1) * a.doss + D) * 2));
-    Tile::template load<4>(lds[buf][0], rq, qbytes, ts, 0, q_hi, wave, lane);
-    Tile::template load<4>(lds[buf][1], ro, obytes, ts, 0, q_hi, wave, lane);
+                  (uint32_t)((q_hi - 1) * obytes + D * 2));
+    Fill::load(dst[0], rq, fq, qbytes, ts, wave);
+    Fill::load(dst[1], ro, fo, obytes, ts, wave);
     if (wave == 0) {
       const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + bh * S, (uint32_t)(S * 4));
       const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.delta + bh * S, (uint32_t)(S * 4));
       const int qrow = min(ts + lane, q_hi - 1);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, CRA_LDS(&sLD[buf][0][0]), 4, qrow * 4, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, CRA_LDS(&sLD[buf][1][0]), 4, qrow * 4, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, CRA_LDS(&dsl[0][0]), 4, qrow * 4, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, CRA_LDS(&dsl[1][0]), 4, qrow * 4, 0, 0, 0);
     }
   };
-  if (ntot > 0) load_tile(0, 0);
+  if (ntot > 0) load_tile(0, stage0, sld0);
 
   auto step = [&](auto BUFC, int it) {
     constexpr int BUF = decltype(BUFC)::value;
+    char(&cur)[2][Tile::kBytes] = BUF ? stage1 : stage0;
+    float(&csl)[2][kBQ] = BUF ? sld1 : sld0;
     wait_vmem();
     __syncthreads();
-    if (it + 1 < ntot) load_tile(it + 1, BUF ^ 1);
+    if (it + 1 < ntot) {
+      if (BUF)
+        load_tile(it + 1, stage0, sld0);
+      else
+        load_tile(it + 1, stage1, sld1);
+    }
     const int j = it / ntile_q;
     const int ts = q_lo + (it - j * ntile_q) * kBQ;
     const int t_last = min(ts + kBQ, q_hi) - 1;
     if (active && t_last >= wq_lo && ts < wq_hi) {
       const bool full = ts >= full_lo && ts + kBQ <= full_hi && ts + kBQ <= q_hi;
       if (full)
-        dkdv2_tile<T, D, false>(lds[BUF][0], lds[BUF][1], sLD[BUF][0], sLD[BUF][1], lo, kf, vf,
-                                dka, dva, c2, g, ts, qmin, qmax);
+        dkdv2_tile<T, D, false>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g, ts,
+                                qmin, qmax);
       else
-        dkdv2_tile<T, D, true>(lds[BUF][0], lds[BUF][1], sLD[BUF][0], sLD[BUF][1], lo, kf, vf,
-                               dka, dva, c2, g, ts, qmin, qmax);
+        dkdv2_tile<T, D, true>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g, ts,
+                               qmin, qmax);
     }
   };
   for (int it = 0; it < ntot; it += 2) {

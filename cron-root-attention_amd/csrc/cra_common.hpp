@@ -233,27 +233,47 @@ struct SwzTile {
     return row * (D * 2) + ((chunk ^ swz(row)) << 4);
   }
 
-  // Cooperative fill by NWAVES waves from a buffer resource whose rows are
-  // row_bytes apart: tile row i <- global row clamp(row0 + i, row_lo,
-  // row_hi - 1). Rows outside [row_lo, row_hi) hold a copy of an edge row;
-  // callers mask them. Each lane needs one 32-bit offset per instruction.
+  // Cooperative fill by NWAVES waves: instruction t = t0 * NWAVES + wave
+  // moves tile rows [4t, 4t + 4) (D = 128; 64 / kCPR rows in general), so a
+  // wave's successive instructions are kRowStep rows apart. kRowStep is a
+  // multiple of the swizzle period, so a lane's in-row chunk is the same for
+  // all of its instructions and its offset is one precomputed VGPR plus a
+  // wave-uniform row offset.
   template <int NWAVES>
-  __device__ __forceinline__ static void load(char* lds, __amdgpu_buffer_rsrc_t rsrc,
-                                              int row_bytes, int row0, int row_lo, int row_hi,
-                                              int wave, int lane) {
-    constexpr int kPer = (kInstr + NWAVES - 1) / NWAVES;
-#pragma unroll
-    for (int t0 = 0; t0 < kPer; ++t0) {
-      const int t = t0 * NWAVES + wave;
-      if (kInstr % NWAVES != 0 && t >= kInstr) break;
-      const int idx = t * 64 + lane;
-      const int row = idx / kCPR;
-      const int chunk = (idx % kCPR) ^ swz(row);
-      const int grow = min(max(row0 + row, row_lo), row_hi - 1);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, CRA_LDS(lds + t * 1024), 16,
-                                               grow * row_bytes + chunk * 16, 0, 0, 0);
+  struct Fill {
+    static constexpr int kPer = (kInstr + NWAVES - 1) / NWAVES;
+    static constexpr int kRowsPerInstr = 64 / kCPR;
+    static constexpr int kRowStep = NWAVES * kRowsPerInstr;
+    static_assert(kPer == 1 || (kRowStep % kRPL == 0 && (kRowStep / kRPL) % kCPR == 0),
+                  "swizzle must repeat every instruction step");
+
+    // Lane's byte offset for its first instruction, relative to tile row 0 of
+    // a source whose rows are row_bytes apart.
+    __device__ __forceinline__ static int lane_off(int wave, int lane, int row_bytes) {
+      const int row = wave * kRowsPerInstr + lane / kCPR;
+      return row * row_bytes + (((lane % kCPR) ^ swz(row)) << 4);
     }
-  }
+
+    // Tile row i <- source row row0 + i. The buffer resource's record count
+    // bounds the rows that may be read: lanes past it load zeros.
+    __device__ __forceinline__ static void load(char* lds, __amdgpu_buffer_rsrc_t rsrc,
+                                                int lane_off, int row_bytes, int row0,
+                                                int wave) {
+      // The LDS destination goes to M0: make the wave index visibly uniform,
+      // and keep its range visible, or the compiler cannot tell this fill
+      // from reads of the other buffer and waits for it before them.
+      static_assert((NWAVES & (NWAVES - 1)) == 0, "power-of-two wave count");
+      const int w = __builtin_amdgcn_readfirstlane(wave) & (NWAVES - 1);
+#pragma unroll
+      for (int t0 = 0; t0 < kPer; ++t0) {
+        const int t = t0 * NWAVES + w;
+        if (kInstr % NWAVES != 0 && t >= kInstr) break;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, CRA_LDS(lds + t * 1024), 16,
+                                                 lane_off + (row0 + t0 * kRowStep) * row_bytes,
+                                                 0, 0, 0);
+      }
+    }
+  };
 
   // 8 consecutive elements (16 B) of `row` starting at column 8*chunk.
   template <typename T>

@@ -253,6 +253,28 @@ struct Fwd2Lane {
   int v[D / 16];   // V^T fragment, columns 16 db ..
 };
 
+template <typename T, int D, int BN>
+__device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& lo,
+                                            const Frag<T> (&qf)[2][D / 32], int kc,
+                                            f32x4 (&s)[2][2]) {
+  using Tile = SwzTile<D, BN>;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int kb = 2 * kc + h;
+    s[h][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s[h][1] = s[h][0];
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.k[c]);
+      s[h][0] = mma(s[h][0], kf, qf[0][c]);
+      s[h][1] = mma(s[h][1], kf, qf[1][c]);
+    }
+  }
+}
+
+// One BN-key tile for the wave's 32 queries, in 32-key halves. The scores of
+// half kc + 1 are issued right after half kc's running-max update, so their
+// MFMAs overlap half kc's exponentials.
 template <typename T, int D, int BN, bool MASK>
 __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, const Fwd2Lane<D>& lo,
                                              const Frag<T> (&qf)[2][D / 32],
@@ -260,22 +282,12 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
                                              float (&l_run)[2], float c2, int g,
                                              const TileMask& mk) {
   using Tile = SwzTile<D, BN>;
+  constexpr int kHalves = BN / 32;
+  f32x4 s[kHalves][2][2];
+  tile_scores<T, D, BN>(tK, lo, qf, 0, s[0]);
 #pragma unroll
-  for (int kc = 0; kc < BN / 32; ++kc) {
-    f32x4 s[2][2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kb = 2 * kc + h;
-      s[h][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      s[h][1] = s[h][0];
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.k[c]);
-        s[h][0] = mma(s[h][0], kf, qf[0][c]);
-        s[h][1] = mma(s[h][1], kf, qf[1][c]);
-      }
-    }
-    Frag<T> pf[2];
+  for (int kc = 0; kc < kHalves; ++kc) {
+    float mu[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       float mx = -__builtin_huge_valf();
@@ -283,8 +295,9 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          if (MASK && !mk.ok(32 * kc + 16 * h + 4 * g + r, qb)) s[h][qb][r] = -__builtin_huge_valf();
-          mx = fmaxf(mx, s[h][qb][r]);
+          if (MASK && !mk.ok(32 * kc + 16 * h + 4 * g + r, qb))
+            s[kc][h][qb][r] = -__builtin_huge_valf();
+          mx = fmaxf(mx, s[kc][h][qb][r]);
         }
       const float ml = mx * c2;
       const bool need = m_run[qb] == -__builtin_huge_valf() ? ml > m_run[qb]
@@ -300,12 +313,18 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
         for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
         m_run[qb] = m_new;
       }
-      const float mu = m_run[qb] == -__builtin_huge_valf() ? 0.f : m_run[qb];
+      mu[qb] = m_run[qb] == -__builtin_huge_valf() ? 0.f : m_run[qb];
+    }
+    if (kc + 1 < kHalves) tile_scores<T, D, BN>(tK, lo, qf, kc + 1, s[kc + 1]);
+    Frag<T> pf[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
       float pv[8];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -mu));
+        for (int r = 0; r < 4; ++r)
+          pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[kc][h][qb][r], c2, -mu[qb]));
       l_run[qb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
       pf[qb] = pack8<T>(pv);
     }
@@ -326,7 +345,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN == 64 ? 
 void fwd2_kernel(FwdArgs a) {
   using Tile = SwzTile<D, BN>;
   constexpr int kBM = 128, kQW = 32, kBN = BN;
-  __shared__ __attribute__((aligned(1024))) char lds[2][2][Tile::kBytes];
+  // Two pipeline stages as separate LDS objects, each selected at compile
+  // time: the compiler can then tell the fill of one stage from reads of the
+  // other and does not wait for the fill before those reads.
+  __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];  // K, V
+  __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -353,24 +376,30 @@ void fwd2_kernel(FwdArgs a) {
   const int nloc = (hi - lo_k + kBN - 1) / kBN;
   const int ntot = nloc + (gmax + kBN - 1) / kBN;
 
-  // Buffer resources over this (b, h)'s rows: 32-bit offsets, uniform bases.
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((S - 1) * a.kss * 2 + D * 2));
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((S - 1) * a.vss * 2 + D * 2));
-  const __amdgpu_buffer_rsrc_t rgk = make_rsrc(gkp, (uint32_t)(a.G * D * 2));
-  const __amdgpu_buffer_rsrc_t rgv = make_rsrc(gvp, (uint32_t)(a.G * D * 2));
+  // Buffer resources over the rows this workgroup may read (local rows below
+  // hi, global rows below gmax): loads past them return zeros. 32-bit
+  // offsets, uniform bases.
+  using Fill = typename Tile::template Fill<4>;
   const int kbytes = (int)(a.kss * 2), vbytes = (int)(a.vss * 2);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((hi - 1) * kbytes + D * 2));
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((hi - 1) * vbytes + D * 2));
+  const __amdgpu_buffer_rsrc_t rgk = make_rsrc(gkp, (uint32_t)(gmax * D * 2));
+  const __amdgpu_buffer_rsrc_t rgv = make_rsrc(gvp, (uint32_t)(gmax * D * 2));
+  const int fk = Fill::lane_off(wave, lane, kbytes);
+  const int fv = Fill::lane_off(wave, lane, vbytes);
+  const int fg = Fill::lane_off(wave, lane, D * 2);
   auto issue = [&](int it, char* dst) {
     if (it < nloc) {
       const int ts = lo_k + it * kBN;
-      Tile::template load<4>(dst, rk, kbytes, ts, 0, hi, wave, lane);
-      Tile::template load<4>(dst + Tile::kBytes, rv, vbytes, ts, 0, hi, wave, lane);
+      Fill::load(dst, rk, fk, kbytes, ts, wave);
+      Fill::load(dst + Tile::kBytes, rv, fv, vbytes, ts, wave);
     } else {
       const int ts = (it - nloc) * kBN;
-      Tile::template load<4>(dst, rgk, D * 2, ts, 0, gmax, wave, lane);
-      Tile::template load<4>(dst + Tile::kBytes, rgv, D * 2, ts, 0, gmax, wave, lane);
+      Fill::load(dst, rgk, fg, D * 2, ts, wave);
+      Fill::load(dst + Tile::kBytes, rgv, fg, D * 2, ts, wave);
     }
   };
-  issue(0, lds[0][0]);
+  issue(0, stage0[0]);
 
   Fwd2Lane<D> lo;
 #pragma unroll
@@ -405,15 +434,17 @@ void fwd2_kernel(FwdArgs a) {
   const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
   const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
 
-  // One loop body for local and global tiles (parameters chosen per tile),
-  // so the accumulators stay in place across iterations.
-  for (int it = 0; it < ntot; ++it) {
-    const int buf = it & 1;
+  // Local and global tiles share one body (parameters chosen per tile); the
+  // loop is unrolled over the two stages.
+  auto step = [&](auto stage_c, int it) {
+    constexpr int kStage = decltype(stage_c)::value;
+    char(&cur)[2][Tile::kBytes] = kStage ? stage1 : stage0;
+    char(&nxt)[2][Tile::kBytes] = kStage ? stage0 : stage1;
     wait_vmem();
     __syncthreads();
-    if (it + 1 < ntot) issue(it + 1, lds[buf ^ 1][0]);
-    const char* tK = lds[buf][0];
-    const char* tV = lds[buf][1];
+    if (it + 1 < ntot) issue(it + 1, nxt[0]);
+    const char* tK = cur[0];
+    const char* tV = cur[1];
     const bool loc = it < nloc;
     const int ts = loc ? lo_k + it * kBN : (it - nloc) * kBN;
     const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
@@ -430,6 +461,10 @@ void fwd2_kernel(FwdArgs a) {
       else
         attend_tile2<T, D, BN, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
     }
+  };
+  for (int it = 0; it < ntot; it += 2) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
   }
 
   T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
