@@ -785,55 +785,55 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   }
 }
 
-// Key-centric dK/dV: each wave owns 32 key rows (rows of k/v, or packed
-// global rows with GLOB), B operands in registers; query tiles of 64 rows of
-// Q and dO stream through LDS with their LSE and Delta. A key row j sees the
-// queries [j, j+W-1] (local) or [first_query(j), S) (global rows), so every
-// mask is a per-key interval.
-template <typename T, int D, bool MASK>
+// Key-centric dK/dV: each wave owns KB blocks of 16 key rows (rows of k/v,
+// or packed global rows with GLOB), B operands in registers; query tiles of
+// 64 rows of Q and dO stream through LDS with their LSE and Delta. A key row
+// j sees the queries [j, j+W-1] (local) or [first_query(j), S) (global rows),
+// so every mask is a per-key interval.
+template <typename T, int D, int KB, bool MASK>
 __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const float* sL,
                                            const float* sDl, const LaneOffs<D>& lo,
-                                           const Frag<T> (&kf)[2][D / 32],
-                                           const Frag<T> (&vf)[2][D / 32],
-                                           f32x4 (&dka)[D / 16][2], f32x4 (&dva)[D / 16][2],
-                                           float c2, int g, int ts, const int (&qmin)[2],
-                                           const int (&qmax)[2]) {
+                                           const Frag<T> (&kf)[KB][D / 32],
+                                           const Frag<T> (&vf)[KB][D / 32],
+                                           f32x4 (&dka)[D / 16][KB], f32x4 (&dva)[D / 16][KB],
+                                           float c2, int g, int ts, const int (&qmin)[KB],
+                                           const int (&qmax)[KB]) {
   using Tile = SwzTile<D, 64>;
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) {
-    float p[2][2][4], ds[2][2][4];  // [qb2][kb][r]
+    float p[2][KB][4], ds[2][KB][4];  // [qb2][kb][r]
 #pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2) {
       const int qblk = 2 * qs + qb2;
-      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, d0 = s0, d1 = s0;
+      f32x4 sc[KB], dp[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) sc[kb] = dp[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         const Frag<T> qa = Tile::template row_frag_at<T>(tQ + qblk * Tile::kBlk16 + lo.row[c]);
         const Frag<T> oa = Tile::template row_frag_at<T>(tO + qblk * Tile::kBlk16 + lo.row[c]);
-        s0 = mma(s0, qa, kf[0][c]);
-        s1 = mma(s1, qa, kf[1][c]);
-        d0 = mma(d0, oa, vf[0][c]);
-        d1 = mma(d1, oa, vf[1][c]);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          sc[kb] = mma(sc[kb], qa, kf[kb][c]);
+          dp[kb] = mma(dp[kb], oa, vf[kb][c]);
+        }
       }
       const f32x4 lq = *reinterpret_cast<const f32x4*>(sL + 16 * qblk + 4 * g) * kLog2e;
       const f32x4 dq = *reinterpret_cast<const f32x4*>(sDl + 16 * qblk + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int qabs = ts + 16 * qblk + 4 * g + r;
-        float x0 = fmaf(s0[r], c2, -lq[r]);
-        float x1 = fmaf(s1[r], c2, -lq[r]);
-        if (MASK) {
-          if (qabs < qmin[0] || qabs > qmax[0]) x0 = -__builtin_huge_valf();
-          if (qabs < qmin[1] || qabs > qmax[1]) x1 = -__builtin_huge_valf();
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          float x = fmaf(sc[kb][r], c2, -lq[r]);
+          if (MASK && (qabs < qmin[kb] || qabs > qmax[kb])) x = -__builtin_huge_valf();
+          p[qb2][kb][r] = __builtin_amdgcn_exp2f(x);
+          ds[qb2][kb][r] = p[qb2][kb][r] * (dp[kb][r] - dq[r]);
         }
-        p[qb2][0][r] = __builtin_amdgcn_exp2f(x0);
-        p[qb2][1][r] = __builtin_amdgcn_exp2f(x1);
-        ds[qb2][0][r] = p[qb2][0][r] * (d0[r] - dq[r]);
-        ds[qb2][1][r] = p[qb2][1][r] * (d1[r] - dq[r]);
       }
     }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       const float pv[8] = {p[0][kb][0], p[0][kb][1], p[0][kb][2], p[0][kb][3],
                            p[1][kb][0], p[1][kb][1], p[1][kb][2], p[1][kb][3]};
       const float sv[8] = {ds[0][kb][0], ds[0][kb][1], ds[0][kb][2], ds[0][kb][3],
@@ -853,10 +853,12 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
   }
 }
 
-template <typename T, int D, bool GLOB>
-__global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
+// NW waves of KB key blocks each cover the workgroup's 128 key rows.
+template <typename T, int D, bool GLOB, int NW, int KB>
+__global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
   using Tile = SwzTile<D, 64>;
-  constexpr int kBK = 128, kKW = 32, kBQ = 64;
+  constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = 64;
+  static_assert(kBK == 128, "128 key rows per workgroup");
   // Two pipeline stages as separate LDS objects (see fwd2_kernel): Q and dO
   // rows, and their LSE and Delta.
   __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];
@@ -909,17 +911,17 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
   const int ntot = ntile_q * grp;
 
   const int qbytes = (int)(a.qss * 2), obytes = (int)(a.doss * 2);
-  using Fill = typename Tile::template Fill<4>;
+  using Fill = typename Tile::template Fill<NW>;
   const int fq = Fill::lane_off(wave, lane, qbytes);
   const int fo = Fill::lane_off(wave, lane, obytes);
 
   const LaneOffs<D> lo = lane_offs<D>(lane);
-  Frag<T> kf[2][D / 32], vf[2][D / 32];
-  int qmin[2], qmax[2];
+  Frag<T> kf[KB][D / 32], vf[KB][D / 32];
+  int qmin[KB], qmax[KB];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < KB; ++kb) {
     const int row = kw + 16 * kb + l16;
-    // tile rows at or past q_hi are clamped copies of row q_hi - 1: excluded
+    // query rows at or past q_hi load as zeros: excluded
     if (GLOB) {
       qmin[kb] = row < nrows ? glob_row_first_query(row, W, a.rpb) : S;
       qmax[kb] = q_hi - 1;
@@ -938,10 +940,11 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
       }
     }
   }
-  f32x4 dka[D / 16][2], dva[D / 16][2];
+  f32x4 dka[D / 16][KB], dva[D / 16][KB];
 #pragma unroll
   for (int db = 0; db < D / 16; ++db)
-    dka[db][0] = dka[db][1] = dva[db][0] = dva[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) dka[db][kb] = dva[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const bool active = kw < nrows;
   const int k_last = min(kw + kKW, nrows) - 1;
@@ -996,11 +999,11 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
     if (active && t_last >= wq_lo && ts < wq_hi) {
       const bool full = ts >= full_lo && ts + kBQ <= full_hi && ts + kBQ <= q_hi;
       if (full)
-        dkdv2_tile<T, D, false>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g, ts,
-                                qmin, qmax);
+        dkdv2_tile<T, D, KB, false>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g,
+                                    ts, qmin, qmax);
       else
-        dkdv2_tile<T, D, true>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g, ts,
-                               qmin, qmax);
+        dkdv2_tile<T, D, KB, true>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g,
+                                   ts, qmin, qmax);
     }
   };
   for (int it = 0; it < ntot; it += 2) {
@@ -1011,7 +1014,7 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
   if (GLOB) {
     float* part = a.gpart + ((int64_t)chunk * nbh + bhk) * a.G * 2 * D;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       const int row = kw + 16 * kb + l16;
       if (row >= nrows) continue;
       float* pk = part + (int64_t)row * 2 * D;
@@ -1027,7 +1030,7 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
   T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh;
   const float rsc = (a.relay && a.rscale) ? a.rscale[hk] : 1.f;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < KB; ++kb) {
     const int j = kw + 16 * kb + l16;
     if (j >= S) continue;
 #pragma unroll
@@ -1067,6 +1070,10 @@ __global__ __launch_bounds__(256) void dkdv2_kernel(BwdArgs a, int ntiles) {
   }
 }
 
+// dK/dV workgroups: 8 waves of 16 key rows (two waves per SIMD, no register
+// file spill into AGPR copies at D = 128).
+constexpr int kDkdvWaves = 8;
+
 template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   using Tr = BwdTraits<T, D>;
@@ -1078,8 +1085,9 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   const int ktiles = (a.S + Tr::kBK - 1) / Tr::kBK;
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((dq2_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv),
-                       dim3(256), 0, st, a, gtiles);
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvWaves, 8 / kDkdvWaves>),
+                       dim3(gtiles * a.nchunk * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a,
+                       gtiles);
   } else {
     hipLaunchKernelGGL((dq_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
     hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv),
@@ -1088,8 +1096,8 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   if (a.dalpha && a.relay)
     hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st,
-                       a, ktiles);
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvWaves, 8 / kDkdvWaves>),
+                       dim3(ktiles * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a, ktiles);
   else
     hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st,
                        a, ktiles);

@@ -272,9 +272,59 @@ __device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& l
   }
 }
 
-// One BN-key tile for the wave's 32 queries, in 32-key halves. The scores of
-// half kc + 1 are issued right after half kc's running-max update, so their
-// MFMAs overlap half kc's exponentials.
+// Largest sum of 8 exponentials accepted against the running maximum: each
+// term is then at most 2^15 and stays finite once rounded to fp16.
+constexpr float kSumMax = 32768.f;
+
+// Exponentials of one 32-key half (8 per lane and query block) against the
+// running maximum, and their sum.
+template <bool MASK>
+__device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float c2, float m,
+                                         int g, const TileMask& mk, float (&pv)[8], float& ps) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (MASK && !mk.ok(32 * kc + 16 * h + 4 * g + r, qb)) s[h][qb][r] = -__builtin_huge_valf();
+      pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -m));
+    }
+  ps = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+}
+
+// Raise the running maximum of query block qb to this half's maximum,
+// rescale its accumulators and redo the half's exponentials. Taken for the
+// first visible keys and whenever a score exceeds the running maximum by
+// enough to push a sum of 8 terms past kSumMax (NaN sums included).
+template <int D>
+__device__ __forceinline__ void half_rescale(f32x4 (&s)[2][2], int qb, float c2,
+                                             f32x4 (&acc)[D / 16][2], float (&m_run)[2],
+                                             float (&l_run)[2], float (&pv)[8], float& ps) {
+  float mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[h][qb][r]);
+  const float m_new = fmaxf(m_run[qb], group_max(mx * c2));
+  const float alpha =
+      m_run[qb] == -__builtin_huge_valf() ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+  l_run[qb] *= alpha;
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
+  m_run[qb] = m_new;
+  const float mu = m_new == -__builtin_huge_valf() ? 0.f : m_new;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -mu));
+  ps = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+}
+
+// One BN-key tile for the wave's 32 queries, in 32-key halves. The online
+// softmax keeps a lazily raised running maximum: exponentials are taken
+// against it first and the maximum is recomputed only when their sum says a
+// term got too large. Program order puts the next half's score MFMAs and the
+// previous half's PV MFMAs beside each half's exponentials, in one basic
+// block, so matrix and vector work can overlap.
 template <typename T, int D, int BN, bool MASK>
 __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, const Fwd2Lane<D>& lo,
                                              const Frag<T> (&qf)[2][D / 32],
@@ -285,56 +335,38 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
   constexpr int kHalves = BN / 32;
   f32x4 s[kHalves][2][2];
   tile_scores<T, D, BN>(tK, lo, qf, 0, s[0]);
+  Frag<T> pf[2];
 #pragma unroll
   for (int kc = 0; kc < kHalves; ++kc) {
-    float mu[2];
+    float pv[2][8], ps[2];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      float mx = -__builtin_huge_valf();
+    for (int qb = 0; qb < 2; ++qb)
+      half_exp<MASK>(s[kc], kc, qb, c2, m_run[qb], g, mk, pv[qb], ps[qb]);
+    if (kc > 0) {
+      // PV of the previous half, beside this half's exponentials
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (MASK && !mk.ok(32 * kc + 16 * h + 4 * g + r, qb))
-            s[kc][h][qb][r] = -__builtin_huge_valf();
-          mx = fmaxf(mx, s[kc][h][qb][r]);
-        }
-      const float ml = mx * c2;
-      const bool need = m_run[qb] == -__builtin_huge_valf() ? ml > m_run[qb]
-                                                            : ml > m_run[qb] + 8.f;
-      if (__any(need)) {
-        const float mt = group_max(ml);
-        const float m_new = fmaxf(m_run[qb], mt);
-        const float alpha = m_run[qb] == -__builtin_huge_valf()
-                                ? 0.f
-                                : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-        l_run[qb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
-        m_run[qb] = m_new;
+      for (int db = 0; db < D / 16; ++db) {
+        const char* pa = tV + (2 * (kc - 1)) * Tile::kBlk16 + lo.v[db];
+        const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+        acc[db][0] = mma(acc[db][0], vt, pf[0]);
+        acc[db][1] = mma(acc[db][1], vt, pf[1]);
       }
-      mu[qb] = m_run[qb] == -__builtin_huge_valf() ? 0.f : m_run[qb];
     }
     if (kc + 1 < kHalves) tile_scores<T, D, BN>(tK, lo, qf, kc + 1, s[kc + 1]);
-    Frag<T> pf[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      float pv[8];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[kc][h][qb][r], c2, -mu[qb]));
-      l_run[qb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-      pf[qb] = pack8<T>(pv);
+      if (__any(!(ps[qb] <= kSumMax)))
+        half_rescale<D>(s[kc], qb, c2, acc, m_run, l_run, pv[qb], ps[qb]);
+      l_run[qb] += ps[qb];
+      pf[qb] = pack8<T>(pv[qb]);
     }
+  }
 #pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
-      const char* pa = tV + (2 * kc) * Tile::kBlk16 + lo.v[db];
-      const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
-      acc[db][0] = mma(acc[db][0], vt, pf[0]);
-      acc[db][1] = mma(acc[db][1], vt, pf[1]);
-    }
+  for (int db = 0; db < D / 16; ++db) {
+    const char* pa = tV + (2 * (kHalves - 1)) * Tile::kBlk16 + lo.v[db];
+    const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+    acc[db][0] = mma(acc[db][0], vt, pf[0]);
+    acc[db][1] = mma(acc[db][1], vt, pf[1]);
   }
 }
 
