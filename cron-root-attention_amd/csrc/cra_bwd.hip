@@ -596,45 +596,50 @@ __device__ __forceinline__ LaneOffs<D> lane_offs(int lane) {
   return o;
 }
 
-template <typename T, int D, bool MASK>
+// Query-centric dQ for QB blocks of 16 queries per wave against one 64-key
+// tile: S = K . Q^T and dP = V . dO^T (key on rows), dS = P * (dP - Delta),
+// dQ^T += K^T . dS^T.
+template <typename T, int D, int QB, bool MASK>
 __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const LaneOffs<D>& lo,
-                                         const Frag<T> (&qf)[2][D / 32],
-                                         const Frag<T> (&df)[2][D / 32], f32x4 (&dqa)[D / 16][2],
-                                         const float (&lse2)[2], const float (&dl)[2], float c2,
-                                         int g, const TileMask& mk) {
+                                         const Frag<T> (&qf)[QB][D / 32],
+                                         const Frag<T> (&df)[QB][D / 32],
+                                         f32x4 (&dqa)[D / 16][QB], const float (&lse2)[QB],
+                                         const float (&dl)[QB], float c2, int g,
+                                         const TileMask& mk) {
   using Tile = SwzTile<D, 64>;
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
-    float ds[2][2][4];  // [h][qb][r]
+    float ds[2][QB][4];  // [h][qb][r]
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int kb = 2 * kc + h;
-      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, p0 = s0, p1 = s0;
+      f32x4 sc[QB], dp[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sc[qb] = dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.row[c]);
         const Frag<T> vf = Tile::template row_frag_at<T>(tV + kb * Tile::kBlk16 + lo.row[c]);
-        s0 = mma(s0, kf, qf[0][c]);
-        s1 = mma(s1, kf, qf[1][c]);
-        p0 = mma(p0, vf, df[0][c]);
-        p1 = mma(p1, vf, df[1][c]);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          sc[qb] = mma(sc[qb], kf, qf[qb][c]);
+          dp[qb] = mma(dp[qb], vf, df[qb][c]);
+        }
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int ko = 16 * kb + 4 * g + r;
-        float x0 = fmaf(s0[r], c2, -lse2[0]);
-        float x1 = fmaf(s1[r], c2, -lse2[1]);
-        if (MASK) {
-          if (!mk.ok(ko, 0)) x0 = -__builtin_huge_valf();
-          if (!mk.ok(ko, 1)) x1 = -__builtin_huge_valf();
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          float x = fmaf(sc[qb][r], c2, -lse2[qb]);
+          if (MASK && !mk.ok(ko, qb)) x = -__builtin_huge_valf();
+          ds[h][qb][r] = __builtin_amdgcn_exp2f(x) * (dp[qb][r] - dl[qb]);
         }
-        ds[h][0][r] = __builtin_amdgcn_exp2f(x0) * (p0[r] - dl[0]);
-        ds[h][1][r] = __builtin_amdgcn_exp2f(x1) * (p1[r] - dl[1]);
       }
     }
-    Frag<T> dsf[2];
+    Frag<T> dsf[QB];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       const float v8[8] = {ds[0][qb][0], ds[0][qb][1], ds[0][qb][2], ds[0][qb][3],
                            ds[1][qb][0], ds[1][qb][1], ds[1][qb][2], ds[1][qb][3]};
       dsf[qb] = pack8<T>(v8);
@@ -643,19 +648,20 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
     for (int db = 0; db < D / 16; ++db) {
       const char* pa = tK + (2 * kc) * Tile::kBlk16 + lo.tr[db];
       const Frag<T> kt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
-      dqa[db][0] = mma(dqa[db][0], kt, dsf[0]);
-      dqa[db][1] = mma(dqa[db][1], kt, dsf[1]);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) dqa[db][qb] = mma(dqa[db][qb], kt, dsf[qb]);
     }
   }
 }
 
-// At least 2 waves per SIMD: the loop body is a single copy of the tile code,
-// which leaves the D = 128 kernel 246 VGPRs and no spills.
-template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+// NW waves of QB blocks of 16 queries each cover the workgroup's 128
+// queries; at least 2 waves per SIMD.
+template <typename T, int D, int NW, int QB>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void dq2_kernel(BwdArgs a, int ntiles) {
   using Tile = SwzTile<D, 64>;
-  constexpr int kBM = 128, kQW = 32, kBN = 64;
+  constexpr int kQW = 16 * QB, kBM = NW * kQW, kBN = 64;
+  static_assert(kBM == 128, "128 queries per workgroup");
   // Two pipeline stages as separate LDS objects (see fwd2_kernel).
   __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];  // K, V
   __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
@@ -687,7 +693,7 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   const int ntot = nloc + (gmax + kBN - 1) / kBN;
   // Buffer resources over the rows this workgroup may read (local rows below
   // hi, global rows below gmax): loads past them return zeros.
-  using Fill = typename Tile::template Fill<4>;
+  using Fill = typename Tile::template Fill<NW>;
   const int kbytes = (int)(a.kss * 2), vbytes = (int)(a.vss * 2);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((hi - 1) * kbytes + D * 2));
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((hi - 1) * vbytes + D * 2));
@@ -710,11 +716,11 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   issue(0, stage0[0]);
 
   const LaneOffs<D> lo = lane_offs<D>(lane);
-  Frag<T> qf[2][D / 32], df[2][D / 32];
-  int qi[2];
-  float lse2[2], dl[2];
+  Frag<T> qf[QB][D / 32], df[QB][D / 32];
+  int qi[QB];
+  float lse2[QB], dl[QB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
     const bool ok = qi[qb] < S;
     lse2[qb] = ok ? a.lse[(int64_t)bh * S + qi[qb]] * kLog2e : 0.f;
@@ -731,16 +737,20 @@ void dq2_kernel(BwdArgs a, int ntiles) {
     }
   }
   const float c2 = a.scale * kLog2e;
-  f32x4 dqa[D / 16][2];
+  f32x4 dqa[D / 16][QB];
 #pragma unroll
-  for (int db = 0; db < D / 16; ++db) dqa[db][0] = dqa[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < D / 16; ++db)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) dqa[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const bool active = q0 < S;
   const int q_last = min(q0 + kQW, S) - 1;
   const int w_lo = max(0, q0 - W + 1);
   const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
   const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
-  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+  int glen[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) glen[qb] = glob_prefix(qi[qb], W, a.rpb);
 
   // Local and global tiles share one body (parameters chosen per tile); the
   // loop is unrolled over the two stages.
@@ -759,15 +769,15 @@ void dq2_kernel(BwdArgs a, int ntiles) {
     const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
     TileMask mk;
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
       mk.hi[qb] = loc ? qi[qb] - ts : glen[qb] - 1 - ts;
       mk.span[qb] = loc ? (unsigned)(W - 1) : 0x7fffffffu;
     }
     if (work) {
       if (full)
-        dq2_tile<T, D, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
+        dq2_tile<T, D, QB, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
       else
-        dq2_tile<T, D, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
+        dq2_tile<T, D, QB, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
     }
   };
   for (int it = 0; it < ntot; it += 2) {
@@ -777,7 +787,7 @@ void dq2_kernel(BwdArgs a, int ntiles) {
 
   T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     if (!active || qi[qb] >= S) continue;
     T* row = dqp + (int64_t)qi[qb] * a.dqss;
 #pragma unroll
@@ -1071,8 +1081,11 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
 }
 
 // dK/dV workgroups: 8 waves of 16 key rows (two waves per SIMD, no register
-// file spill into AGPR copies at D = 128).
+// file spill into AGPR copies at D = 128). dQ workgroups: 4 waves of 32
+// queries (each K/V fragment read from LDS serves two query blocks; 8 waves
+// of 16 queries measured 27% slower at D = 128).
 constexpr int kDkdvWaves = 8;
+constexpr int kDqWaves = 4;
 
 template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
@@ -1084,7 +1097,8 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   const int gtiles = (int)((a.G + Tr::kBK - 1) / Tr::kBK);
   const int ktiles = (a.S + Tr::kBK - 1) / Tr::kBK;
   if constexpr (sizeof(T) == 2) {
-    hipLaunchKernelGGL((dq2_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
+    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, 8 / kDqWaves>), dim3(qtiles * a.B * a.Hq),
+                       dim3(64 * kDqWaves), 0, st, a, qtiles);
     hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvWaves, 8 / kDkdvWaves>),
                        dim3(gtiles * a.nchunk * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a,
                        gtiles);
