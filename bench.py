@@ -45,6 +45,17 @@ def pairs_fast(S: int, top_k: int = 2) -> int:
     return int(p.sum())
 
 
+def phase_pairs(S: int, top_k: int = 2) -> dict:
+    """Pairs per (b, h) by phase: local window, strided rows, relay rows."""
+    import numpy as np
+    W = int(math.ceil(math.sqrt(S)))
+    i = np.arange(S, dtype=np.int64)
+    ls = np.maximum(i - W + 1, 0)
+    return {"local": int(np.minimum(i + 1, W).sum()),
+            "strided": int(((ls + W - 1) // W).sum()),
+            "relay": int((top_k * (ls // W)).sum()) if S > 2048 else 0}
+
+
 def row_pairs(rows, S, top_k=2):
     import numpy as np
     W = int(math.ceil(math.sqrt(S)))
@@ -158,6 +169,35 @@ def run_main(args):
             "traffic": traffic_for("fwd", workload), "avg_ms": round(kern_ms, 4),
             "algorithmic_flops": f_fwd}
 
+    # per-phase forward (cra_fwd_phases) and the global-row build (K1)
+    pp = phase_pairs(S)
+    t_loc = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_LOCAL),
+                          args.steps, args.warmup, torch)
+    t_glob = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv,
+                                                   phases=_native.PHASE_GLOBAL),
+                           args.steps, args.warmup, torch)
+    t_bg = per_launch_ms(lambda: _native.build_global(p, k, v, None), args.steps, args.warmup,
+                         torch)
+    G = int(_native.global_rows(p))
+    NB = (S + W - 1) // W
+    e = 2
+    bg_bytes = B * H * (S * D * e + G * D * e + 2 * G * D * e + 4 * NB * 2)
+    f_loc = 4 * D * pp["local"] * B * H
+    f_glob = 4 * D * (pp["strided"] + pp["relay"]) * B * H
+    phases = {
+        "local": {"ms": round(t_loc, 4), "pairs_per_head": pp["local"],
+                  "tflops": round(f_loc / (t_loc * 1e-3) / 1e12, 2),
+                  "mfma_frac": round(f_loc / (t_loc * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
+        "global": {"ms": round(t_glob, 4),
+                   "pairs_per_head": pp["strided"] + pp["relay"],
+                   "strided_pairs_per_head": pp["strided"], "relay_pairs_per_head": pp["relay"],
+                   "tflops": round(f_glob / (t_glob * 1e-3) / 1e12, 2),
+                   "mfma_frac": round(f_glob / (t_glob * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
+        "build_global": {"ms": round(t_bg, 4), "bytes": bg_bytes,
+                         "GBps": round(bg_bytes / (t_bg * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(bg_bytes / (t_bg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+    }
+
     cpu = None
     if not args.skip_cpu:
         cpu = cpu_baseline(B, H, S, D, args.cpu_seconds, args.cpu_threads)
@@ -172,7 +212,7 @@ def run_main(args):
                    "B": B, "H": H, "S": S, "D": D, "window": W, "relay_top_k": 2},
         "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 3),
         "fwdbwd_ms": round(step_ms, 4), "fwdbwd_tflops": round(f_all / (step_ms * 1e-3) / 1e12, 3),
-        "pairs_per_head": P, "roofline": roof, "cpu_baseline": cpu,
+        "pairs_per_head": P, "roofline": roof, "phases": phases, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 
@@ -205,21 +245,63 @@ def run_profile_workload(args):
     print(json.dumps({"profile_workload": "done", "B": B, "H": H, "S": S, "D": D}), flush=True)
 
 
+def sdpa_backend(q, k, v, torch, F):
+    """First fused SDPA backend that runs this shape (flash, then memory
+    efficient). The math backend is never used: its batched products on
+    transposed bf16 views are unsafe on this platform."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for b in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel([b]):
+                F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            torch.cuda.synchronize()
+            return b
+        except RuntimeError:
+            continue
+    return None
+
+
+def first_win(points, key_a, key_b):
+    """Smallest S from which a is faster than b at every larger swept S."""
+    win = None
+    for pt in sorted(points, key=lambda x: -x["S"]):
+        if pt.get(key_b) is None or pt[key_a] < pt[key_b]:
+            win = pt["S"]
+        else:
+            break
+    return win
+
+
 def run_crossover(args):
+    """S sweep of the sqrt(N) op against ROCm SDPA (causal), forward and
+    forward+backward, for the BASELINE head shapes; one JSON line per point
+    and one summary line per shape with the crossover S of each mode."""
     import torch
     import torch.nn.functional as F
+    from torch.nn.attention import sdpa_kernel
     import cron_root_attention as cra
     dev = torch.device("cuda", 0)
-    for (B, H, D, dtype) in ((2, 32, 128, torch.bfloat16), (1, 16, 128, torch.float16),
-                             (1, 8, 64, torch.float16)):
-        for S in (256, 512, 768, 1024, 1536, 2048, 3072, 4096, 8192, 16384):
+    shapes = ((2, 32, 128, torch.bfloat16), (1, 16, 128, torch.float16),
+              (1, 8, 64, torch.float16), (1, 12, 64, torch.float16))
+    seqs = (256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384)
+    for (B, H, D, dtype) in shapes:
+        points = []
+        backend = None
+        for S in seqs:
             g = torch.Generator(device=dev).manual_seed(0)
             q, k, v, do = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=dtype)
                            for _ in range(4))
-            res = {"B": B, "H": H, "D": D, "S": S, "dtype": str(dtype).split(".")[-1]}
-            for name, fn in (("cra", lambda a, b, c: cra.cron_root_attention(a, b, c)),
-                             ("sdpa", lambda a, b, c: F.scaled_dot_product_attention(
-                                 a, b, c, is_causal=True))):
+            if backend is None:
+                backend = sdpa_backend(q, k, v, torch, F)
+            res = {"B": B, "H": H, "D": D, "S": S, "dtype": str(dtype).split(".")[-1],
+                   "sdpa_backend": str(backend).split(".")[-1] if backend is not None else None}
+            impls = [("cra", lambda a, b, c: cra.cron_root_attention(a, b, c))]
+            if backend is not None:
+                def sd(a, b, c, _b=backend):
+                    with sdpa_kernel([_b]):
+                        return F.scaled_dot_product_attention(a, b, c, is_causal=True)
+                impls.append(("sdpa", sd))
+            for name, fn in impls:
                 with torch.no_grad():
                     res[f"{name}_fwd_ms"] = round(timed(lambda: fn(q, k, v), 20, 5, torch), 4)
                 qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
@@ -228,7 +310,13 @@ def run_crossover(args):
                     qg.grad = kg.grad = vg.grad = None
                     fn(qg, kg, vg).backward(do)
                 res[f"{name}_train_ms"] = round(timed(st, 10, 3, torch), 4)
+            points.append(res)
             print(json.dumps(res), flush=True)
+        summary = {"crossover": True, "B": B, "H": H, "D": D, "dtype": str(dtype).split(".")[-1],
+                   "sdpa_backend": points[0]["sdpa_backend"],
+                   "fwd_crossover_S": first_win(points, "cra_fwd_ms", "sdpa_fwd_ms"),
+                   "train_crossover_S": first_win(points, "cra_train_ms", "sdpa_train_ms")}
+        print(json.dumps(summary), flush=True)
 
 
 def main(argv=None):

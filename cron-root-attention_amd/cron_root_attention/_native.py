@@ -70,6 +70,9 @@ _SIGNATURES = {
                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "cra_fwd": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
                                ctypes.c_void_p, CraTensor, ctypes.c_void_p, ctypes.c_void_p]),
+    "cra_fwd_phases": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
+                                      ctypes.c_void_p, CraTensor, ctypes.c_void_p, ctypes.c_int32,
+                                      ctypes.c_void_p]),
     "cra_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
     "cra_bwd": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, CraTensor, CraTensor,
                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -182,13 +185,23 @@ def build_global(p: CraProblem, k: torch.Tensor, v: torch.Tensor,
     return gk, gv, src
 
 
-def forward(p: CraProblem, q, k, v, gk, gv):
+PHASE_LOCAL = 1
+PHASE_GLOBAL = 2
+
+
+def forward(p: CraProblem, q, k, v, gk, gv, phases: int = PHASE_LOCAL | PHASE_GLOBAL):
+    """cra_fwd (all phases) or cra_fwd_phases (a subset, for measurement)."""
     lib = load_library()
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(p.B, p.H_q, p.S, dtype=torch.float32, device=q.device)
-    _check(lib.cra_fwd(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
-                       gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(), _stream(q)),
-           "cra_fwd")
+    if phases == PHASE_LOCAL | PHASE_GLOBAL:
+        _check(lib.cra_fwd(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                           gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(),
+                           _stream(q)), "cra_fwd")
+    else:
+        _check(lib.cra_fwd_phases(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                                  gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(),
+                                  phases, _stream(q)), "cra_fwd_phases")
     return o, lse
 
 

@@ -1,11 +1,14 @@
 """SDPA / sqrt(N) dispatch by sequence length (reference hybrid.py:1-124).
 
 The reference's crossover (1536 tokens, hybrid.py:22) was measured on an RTX
-5070 Ti.  Here the crossover is a gfx950 table, measured on one MI355X with
-``bench.py --crossover`` against ROCm's ``scaled_dot_product_attention``
-(forward and forward+backward separately, per head dim); see
-``CROSSOVER_GFX950``.  ``_SDPA_THRESHOLD`` is the training (fwd+bwd)
-crossover at D=128, the reference's role for the constant.
+5070 Ti.  Here the crossover is a gfx950 table measured on one MI355X with
+``bench.py --crossover`` against ROCm's fused (flash) SDPA, causal, for
+forward and forward+backward separately: ``CROSSOVER_GFX950``.  Below a few
+thousand tokens the sqrt(N) op costs its launch floor (about 37 us forward,
+180 us forward+backward) while SDPA grows with B*H*S^2, so the crossover
+falls as B*H grows; the table keeps one row per measured B*H.
+``_SDPA_THRESHOLD`` is the forward+backward crossover at D=128 for B*H=16,
+the role of the reference's constant.
 """
 from __future__ import annotations
 
@@ -17,23 +20,31 @@ import torch.nn.functional as F
 
 from .core import cron_root_attention_v14
 
-# (mode, head_dim) -> smallest S at which the sqrt(N) kernel beats SDPA on
-# MI355X (bf16/fp16, causal). Filled from the measured sweep.
+# (mode, head_dim, smallest B*H the row applies to) -> smallest swept S from
+# which the sqrt(N) op beats SDPA at every larger swept S. Sweep: S in
+# {256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384};
+# shapes (B, H, D, dtype) = (1, 16, 128, fp16), (2, 32, 128, bf16),
+# (1, 8, 64, fp16), (1, 12, 64, fp16).
 CROSSOVER_GFX950 = {
-    ("fwd", 64): 1536,
-    ("fwd", 128): 1536,
-    ("train", 64): 1536,
-    ("train", 128): 1536,
+    ("fwd", 128, 1): 768,      # B=1 H=16 fp16 (fwd 0.037 vs 0.044 ms at S=768)
+    ("fwd", 128, 64): 512,     # B=2 H=32 bf16 (0.038 vs 0.041 ms at S=512)
+    ("train", 128, 1): 1024,   # B=1 H=16 fp16 (0.181 vs 0.199 ms at S=1024)
+    ("train", 128, 64): 512,   # B=2 H=32 bf16 (0.182 vs 0.191 ms at S=512)
+    ("fwd", 64, 1): 1536,      # B=1 H=8 and H=12 fp16
+    ("train", 64, 1): 2048,    # B=1 H=8 and H=12 fp16
 }
-_SDPA_THRESHOLD = CROSSOVER_GFX950[("train", 128)]
+_SDPA_THRESHOLD = CROSSOVER_GFX950[("train", 128, 1)]
 
 
-def crossover(head_dim: int, training: bool) -> int:
-    """Measured gfx950 crossover for the nearest tabulated head dim."""
+def crossover(head_dim: int, training: bool, batch_heads: int = 1) -> int:
+    """Measured gfx950 crossover for the nearest tabulated head dim and the
+    largest tabulated B*H not above ``batch_heads``."""
     mode = "train" if training else "fwd"
-    dims = sorted({d for (m, d) in CROSSOVER_GFX950 if m == mode})
+    dims = sorted({d for (m, d, _) in CROSSOVER_GFX950 if m == mode})
     d = min(dims, key=lambda x: abs(x - head_dim))
-    return CROSSOVER_GFX950[(mode, d)]
+    rows = sorted(bh for (m, dd, bh) in CROSSOVER_GFX950 if m == mode and dd == d)
+    bh = max([r for r in rows if r <= max(1, batch_heads)] or rows[:1])
+    return CROSSOVER_GFX950[(mode, d, bh)]
 
 
 def cron_root_attention_hybrid(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -50,7 +61,8 @@ def cron_root_attention_hybrid(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     if backend != "auto":
         raise ValueError(f"unknown backend {backend!r}")
     if threshold is None:
-        threshold = crossover(q.shape[-1], torch.is_grad_enabled() and q.requires_grad)
+        threshold = crossover(q.shape[-1], torch.is_grad_enabled() and q.requires_grad,
+                              q.shape[0] * q.shape[1])
     if S >= threshold:
         return cron_root_attention_v14(q, k, v)
     return F.scaled_dot_product_attention(q, k, v, is_causal=True)

@@ -55,7 +55,8 @@ class CronRootAttention(nn.Module):
             return False
         thr = self.threshold
         if thr is None:
-            thr = crossover(self.head_dim, self.training and torch.is_grad_enabled())
+            thr = crossover(self.head_dim, self.training and torch.is_grad_enabled(),
+                            x.shape[0] * self.n_heads)
         return S < thr
 
     def forward(self, x: torch.Tensor, kv: Optional[torch.Tensor] = None) -> torch.Tensor:

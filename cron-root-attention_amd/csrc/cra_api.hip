@@ -128,7 +128,16 @@ int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glo
 
 int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, const void* glob_k,
             const void* glob_v, cra_tensor o, float* lse, void* stream) {
+  return cra_fwd_phases(p, q, k, v, glob_k, glob_v, o, lse, CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL,
+                        stream);
+}
+
+int cra_fwd_phases(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+                   const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                   int32_t phase_mask, void* stream) {
   if (int e = check_problem(p)) return e;
+  if (phase_mask < 1 || phase_mask > (CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL))
+    return fail(CRA_E_INVALID, "phase_mask must be a non-empty subset of CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL");
   const int esz = elem_size(p->dtype);
   if (int e = check_tensor("q", q, esz)) return e;
   if (int e = check_tensor("k", k, esz)) return e;
@@ -150,6 +159,7 @@ int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cons
   a.G = num_blocks(p) * a.rpb;
   a.scale = p->scale;
   a.ntiles = (p->S + 127) / 128;
+  a.phases = phase_mask;
   hipError_t e = cra::launch_fwd(p->dtype, p->D, a, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "cra_fwd launch");
   return CRA_OK;
@@ -176,6 +186,11 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
   if (int e = check_tensor("dq", dq, esz)) return e;
   if (int e = check_tensor("dk", dk, esz)) return e;
   if (int e = check_tensor("dv", dv, esz)) return e;
+  // the backward reads these through buffer resources with 32-bit offsets
+  if (int e = check_span("q", q, p, esz)) return e;
+  if (int e = check_span("k", k, p, esz)) return e;
+  if (int e = check_span("v", v, p, esz)) return e;
+  if (int e = check_span("dout", dout, p, esz)) return e;
   if (int e = check_buf("lse", lse)) return e;
   if (int e = check_buf("glob_k", glob_k)) return e;
   if (int e = check_buf("glob_v", glob_v)) return e;

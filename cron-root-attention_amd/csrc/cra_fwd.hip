@@ -174,7 +174,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   const int lo = max(0, m0 - W + 1);
   const int hi = min(S, m0 + Tr::kBM);
   const int w_lo = max(0, q0 - W + 1);
-  for (int ts = lo; ts < hi; ts += Tr::kBN) {
+  const int hi_loc = (a.phases & 1) ? hi : lo;
+  for (int ts = lo; ts < hi_loc; ts += Tr::kBN) {
     stk.load(kp, a.kss, ts, 0, hi, tid);
     stv.load(vp, a.vss, ts, 0, hi, tid);
     __syncthreads();
@@ -199,7 +200,8 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
   const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
   const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
-  for (int ts = 0; ts < gmax; ts += Tr::kBN) {
+  const int g_end = (a.phases & 2) ? gmax : 0;
+  for (int ts = 0; ts < g_end; ts += Tr::kBN) {
     stk.load(gkp, D, ts, 0, gmax, tid);
     stv.load(gvp, D, ts, 0, gmax, tid);
     __syncthreads();
@@ -405,8 +407,8 @@ void fwd2_kernel(FwdArgs a) {
   const int lo_k = max(0, m0 - W + 1);
   const int hi = min(S, m0 + kBM);
   const int gmax = glob_prefix(hi - 1, W, a.rpb);
-  const int nloc = (hi - lo_k + kBN - 1) / kBN;
-  const int ntot = nloc + (gmax + kBN - 1) / kBN;
+  const int nloc = (a.phases & 1) ? (hi - lo_k + kBN - 1) / kBN : 0;
+  const int ntot = nloc + ((a.phases & 2) ? (gmax + kBN - 1) / kBN : 0);
 
   // Buffer resources over the rows this workgroup may read (local rows below
   // hi, global rows below gmax): loads past them return zeros. 32-bit

@@ -32,6 +32,7 @@ struct FwdArgs {
   int64_t G;
   float scale;
   int ntiles;
+  int phases;  // bit 0: local window, bit 1: global rows
 };
 
 struct BwdArgs {

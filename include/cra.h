@@ -102,6 +102,20 @@ int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glo
 int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
             const void* glob_k, const void* glob_v, cra_tensor o, float* lse, void* stream);
 
+/* Key phases for cra_fwd_phases. */
+#define CRA_PHASE_LOCAL 1  /* the local window [ls, i] */
+#define CRA_PHASE_GLOBAL 2 /* the packed strided and relay rows */
+
+/* cra_fwd over a subset of the key phases: o and lse are the attention of
+ * each query over the keys of the selected phases only (a query with no such
+ * key gets o = 0, lse = -inf). phase_mask = CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL
+ * is cra_fwd. No counterpart in the reference, whose forward interleaves the
+ * phases in one kernel (core.py:976-1142); it exists so that the MFMA
+ * utilisation of each phase can be measured on its own. */
+int cra_fwd_phases(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+                   const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                   int32_t phase_mask, void* stream);
+
 /* Workspace the backward needs, in bytes (0 is possible). */
 size_t cra_bwd_workspace_bytes(const cra_problem* p);
 

@@ -240,7 +240,7 @@ def relay_select(k: torch.Tensor, plan: Plan, norm: str = "lanetree") -> torch.T
 def forward(q, k, v, plan: Plan, kv_groups: int = 1, src: Optional[torch.Tensor] = None,
             relay_scale: Optional[torch.Tensor] = None, chunk: int = 256,
             norm: str = "lanetree", rows: Optional[tuple] = None,
-            relay_dtype: Optional[torch.dtype] = None):
+            relay_dtype: Optional[torch.dtype] = None, phases: str = "all"):
     """Exact softmax over each query's multiset, fp64, differentiable.
 
     q: [B, Hq, S, D]; k, v: [B, Hkv, S, D]; query head h reads kv head
@@ -250,8 +250,13 @@ def forward(q, k, v, plan: Plan, kv_groups: int = 1, src: Optional[torch.Tensor]
     reference's in-dtype multiply does (the rounding is not differentiated).
     ``rows=(lo, hi)`` computes only queries [lo, hi) (outputs then hold those
     rows) so long sequences can be spot-checked.
+    ``phases`` = "local" or "global" restricts the multiset to the local
+    window or to the strided and relay rows (the subsets the build's
+    measurement entry point cra_fwd_phases computes); a query with an empty
+    subset gets o = 0 and lse = -inf.
     Returns (o [B,Hq,S,D] fp64, lse [B,Hq,S] fp64, src).
     """
+    assert phases in ("all", "local", "global")
     q = q.to(torch.float64)
     k = k.to(torch.float64)
     v = v.to(torch.float64)
@@ -297,16 +302,24 @@ def forward(q, k, v, plan: Plan, kv_groups: int = 1, src: Optional[torch.Tensor]
         m_loc = (kj[None, :] >= ls[:, None]) & (kj[None, :] <= qi[:, None])
         s_str = qc @ Ks.transpose(-1, -2) * scale
         m_str = stride_idx[None, :] < ls[:, None]
+        if phases == "global":
+            m_loc = torch.zeros_like(m_loc)
+        if phases == "local":
+            m_str = torch.zeros_like(m_str)
         parts_s = [s_loc.masked_fill(~m_loc, -math.inf), s_str.masked_fill(~m_str, -math.inf)]
         parts_v = [ve[:, :, w0:c1], Vs]
         if plan.relay:
             s_rel = qc @ Kr.transpose(-1, -2) * scale
             m_rel = r_end[None, :] < ls[:, None]
+            if phases == "local":
+                m_rel = torch.zeros_like(m_rel)
             parts_s.append(s_rel.masked_fill(~m_rel, -math.inf))
             parts_v.append(Vr)
         s_all = torch.cat(parts_s, dim=-1)
         lse = torch.logsumexp(s_all, dim=-1)
         p = torch.exp(s_all - lse.unsqueeze(-1))
+        if phases != "all":  # empty subsets: 0 instead of 0/0
+            p = torch.where(torch.isfinite(lse).unsqueeze(-1), p, torch.zeros_like(p))
         o = sum(p[..., off:off + pv.shape[2]] @ pv
                 for off, pv in zip(np.cumsum([0] + [x.shape[2] for x in parts_v[:-1]]), parts_v))
         outs.append(o)

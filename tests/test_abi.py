@@ -86,6 +86,38 @@ def test_fwd_rejects_bad_layout():
     assert lib.cra_fwd(p, good, good, good, 0x10000, 0x10000, good, None, None) == N.E_INVALID
 
 
+def test_fwd_phases_rejects_bad_mask():
+    lib = N.load_library()
+    good = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    p = ctypes.byref(prob())
+    for mask in (0, 4, -1, 7):
+        rc = lib.cra_fwd_phases(p, good, good, good, 0x10000, 0x10000, good, 0x10000, mask, None)
+        assert rc == N.E_INVALID, mask
+        assert "phase_mask" in lib.cra_last_error().decode()
+
+
+def test_head_span_limit():
+    # k and v are read through buffer resources with 32-bit offsets: a head
+    # spanning 2^31 bytes or more is rejected (the Python layer then passes a
+    # contiguous copy)
+    lib = N.load_library()
+    good = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    wide = N.CraTensor(0x10000, 1 << 40, 1 << 35, 1 << 18)  # row stride 512 KiB elements
+    p = ctypes.byref(prob())
+    assert lib.cra_fwd(p, good, wide, good, 0x10000, 0x10000, good, 0x10000, None) == N.E_LAYOUT
+    assert "2^31" in lib.cra_last_error().decode()
+    need = lib.cra_bwd_workspace_bytes(p)
+    for pos in range(3):
+        args = [good] * 3
+        args[pos] = wide
+        rc = lib.cra_bwd(p, *args, good, good, 0x10000, 0x10000, 0x10000, 0x10000, None, good,
+                         good, good, None, 0x10000, need, None)
+        assert rc == N.E_LAYOUT and "2^31" in lib.cra_last_error().decode(), pos
+    rc = lib.cra_bwd(p, good, good, good, good, wide, 0x10000, 0x10000, 0x10000, 0x10000, None,
+                     good, good, good, None, 0x10000, need, None)
+    assert rc == N.E_LAYOUT and "dout" in lib.cra_last_error().decode()
+
+
 def test_bwd_rejects_small_workspace():
     lib = N.load_library()
     t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)

@@ -88,3 +88,22 @@ def test_gpu_info_without_gpu():
         pytest.skip("GPU present")
     assert cra.get_gpu_info() == {"gpu_name": "No GPU", "sm_count": 0, "is_known_gpu": False}
     assert cra.get_num_sms() == 1
+
+
+def test_crossover_table_lookup():
+    from cron_root_attention.hybrid import CROSSOVER_GFX950, _SDPA_THRESHOLD, crossover
+    # measured rows are returned as measured
+    for (mode, d, bh), s in CROSSOVER_GFX950.items():
+        assert crossover(d, mode == "train", bh) == s
+    # larger B*H uses the largest measured row not above it; smaller falls back to the first
+    assert crossover(128, True, 4096) == CROSSOVER_GFX950[("train", 128, 64)]
+    assert crossover(128, False, 8) == CROSSOVER_GFX950[("fwd", 128, 1)]
+    # nearest head dim
+    assert crossover(96, True, 16) == CROSSOVER_GFX950[("train", 128, 1)]
+    assert crossover(32, False, 16) == CROSSOVER_GFX950[("fwd", 64, 1)]
+    assert _SDPA_THRESHOLD == CROSSOVER_GFX950[("train", 128, 1)]
+    # more parallel work never raises the crossover
+    for mode in ("fwd", "train"):
+        for d in (64, 128):
+            seq = [crossover(d, mode == "train", bh) for bh in (1, 16, 64, 1024)]
+            assert seq == sorted(seq, reverse=True)

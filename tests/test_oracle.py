@@ -217,6 +217,27 @@ def test_forward_row_range_matches_full():
     assert torch.allclose(lf[:, :, 2500:2800], lp, atol=1e-13)
 
 
+def test_forward_phase_subsets_merge_to_full():
+    """The local-only and global-only restrictions, merged with their
+    log-sum-exp weights, give the full forward (softmax over a disjoint
+    union); a query before the first global row has an empty global subset."""
+    torch.manual_seed(5)
+    S, D = 3000, 16
+    q, k, v = (torch.randn(1, 2, S, D) for _ in range(3))
+    plan = O.make_plan(S)
+    o_all, l_all, src = O.forward(q, k, v, plan)
+    o_l, l_l, _ = O.forward(q, k, v, plan, src=src, phases="local")
+    o_g, l_g, _ = O.forward(q, k, v, plan, src=src, phases="global")
+    lse = torch.logaddexp(l_l, l_g)
+    fin = torch.isfinite(l_g).unsqueeze(-1)
+    merged = torch.exp(l_l - lse).unsqueeze(-1) * o_l + torch.where(
+        fin, torch.exp(l_g - lse).unsqueeze(-1) * o_g, torch.zeros_like(o_g))
+    assert torch.allclose(merged, o_all, atol=1e-12)
+    assert torch.allclose(lse, l_all, atol=1e-12)
+    assert bool(torch.isinf(l_g[..., :plan.W]).all()) and bool((o_g[:, :, :plan.W] == 0).all())
+    assert bool(torch.isfinite(l_g[..., plan.W:]).all())
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 def test_golden_cpu_reference_mode(shape):
     z = fixture(shape)

@@ -164,6 +164,26 @@ def test_forward_matches_oracle(case):
         assert max_abs(lse, ref_lse) <= tol
 
 
+@pytest.mark.parametrize("dtype,S,D", [(F16, 3000, 128), (BF16, 2500, 64), (F32, 2300, 32),
+                                       (F16, 1500, 64)])
+def test_forward_phase_subsets(dtype, S, D):
+    """cra_fwd_phases (the per-phase measurement entry point): the local-only
+    and global-only forwards each match the oracle restricted to that phase."""
+    say(f"forward phases {dtype} S={S} D={D}")
+    B, H = 1, 2
+    q, k, v, _ = inputs(B, H, H, S, D, dtype, seed=S + 3 * D)
+    plan = plan_for(S)
+    p = _native.problem(B, H, H, S, D, plan.W, plan.relay, plan.top_k, dtype, 1 / math.sqrt(D))
+    gk, gv, _ = _native.build_global(p, k.to(DEV), v.to(DEV), None)
+    for name, mask in (("local", _native.PHASE_LOCAL), ("global", _native.PHASE_GLOBAL)):
+        o, lse = _native.forward(p, q.to(DEV), k.to(DEV), v.to(DEV), gk, gv, phases=mask)
+        ref, ref_lse = check_forward(o, q, k, v, plan, dtype, phases=name)
+        fin = torch.isfinite(ref_lse)
+        assert torch.equal(torch.isfinite(lse.cpu()), fin)
+        tol = 1e-3 if dtype != F32 else 1e-5
+        assert max_abs(lse.cpu()[fin], ref_lse[fin]) <= tol
+
+
 def test_forward_strided_views_and_relay_scale():
     say("forward strided views + relay_log_scale")
     B, S, H, D = 1, 3000, 4, 64
