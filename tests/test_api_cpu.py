@@ -99,7 +99,7 @@ def test_crossover_table_lookup():
     assert crossover(128, True, 4096) == CROSSOVER_GFX950[("train", 128, 64)]
     assert crossover(128, False, 8) == CROSSOVER_GFX950[("fwd", 128, 1)]
     # nearest head dim
-    assert crossover(96, True, 16) == CROSSOVER_GFX950[("train", 128, 1)]
+    assert crossover(112, True, 16) == CROSSOVER_GFX950[("train", 128, 1)]
     assert crossover(32, False, 16) == CROSSOVER_GFX950[("fwd", 64, 1)]
     assert _SDPA_THRESHOLD == CROSSOVER_GFX950[("train", 128, 1)]
     # more parallel work never raises the crossover
