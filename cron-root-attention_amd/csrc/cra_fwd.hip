@@ -372,13 +372,14 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
   }
 }
 
-// BN: key rows per LDS tile (64: 2 x 32 KB double buffer, 2 waves/SIMD;
-// 32: 2 x 16 KB, 3 waves/SIMD).
-template <typename T, int D, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BN == 64 ? 2 : 3, BN == 64 ? 2 : 3)))
+// NW waves of 32 queries share each K/V tile of BN = 64 rows (2 x 32 KB
+// double buffer at D = 128); at least 2 waves per SIMD.
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fwd2_kernel(FwdArgs a) {
+  constexpr int BN = 64;
   using Tile = SwzTile<D, BN>;
-  constexpr int kBM = 128, kQW = 32, kBN = BN;
+  constexpr int kQW = 32, kBM = NW * kQW, kBN = BN;
   // Two pipeline stages as separate LDS objects, each selected at compile
   // time: the compiler can then tell the fill of one stage from reads of the
   // other and does not wait for the fill before those reads.
@@ -413,7 +414,7 @@ void fwd2_kernel(FwdArgs a) {
   // Buffer resources over the rows this workgroup may read (local rows below
   // hi, global rows below gmax): loads past them return zeros. 32-bit
   // offsets, uniform bases.
-  using Fill = typename Tile::template Fill<4>;
+  using Fill = typename Tile::template Fill<NW>;
   const int kbytes = (int)(a.kss * 2), vbytes = (int)(a.vss * 2);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kp, (uint32_t)((hi - 1) * kbytes + D * 2));
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vp, (uint32_t)((hi - 1) * vbytes + D * 2));
@@ -520,20 +521,25 @@ void fwd2_kernel(FwdArgs a) {
   }
 }
 
+// Waves per forward workgroup (32 queries each) for 2-byte types. 8 waves
+// (256 queries sharing each K/V tile) halve the tile loads per query but
+// measured 4% slower at D = 128: the wider local window adds key tiles.
+constexpr int kFwdWaves = 4;
+
 template <typename T>
 hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
-  dim3 grid(a.ntiles * a.B * a.Hq);
   if constexpr (sizeof(T) == 2) {
-#ifndef CRA_FWD_BN
-#define CRA_FWD_BN 64
-#endif
+    FwdArgs b = a;
+    b.ntiles = (a.S + 32 * kFwdWaves - 1) / (32 * kFwdWaves);
+    const dim3 grid(b.ntiles * b.B * b.Hq), block(64 * kFwdWaves);
     switch (D) {
-      case 32: hipLaunchKernelGGL((fwd2_kernel<T, 32, CRA_FWD_BN>), grid, dim3(256), 0, st, a); break;
-      case 64: hipLaunchKernelGGL((fwd2_kernel<T, 64, CRA_FWD_BN>), grid, dim3(256), 0, st, a); break;
-      case 128: hipLaunchKernelGGL((fwd2_kernel<T, 128, CRA_FWD_BN>), grid, dim3(256), 0, st, a); break;
+      case 32: hipLaunchKernelGGL((fwd2_kernel<T, 32, kFwdWaves>), grid, block, 0, st, b); break;
+      case 64: hipLaunchKernelGGL((fwd2_kernel<T, 64, kFwdWaves>), grid, block, 0, st, b); break;
+      case 128: hipLaunchKernelGGL((fwd2_kernel<T, 128, kFwdWaves>), grid, block, 0, st, b); break;
       default: return hipErrorInvalidValue;
     }
   } else {
+    const dim3 grid(a.ntiles * a.B * a.Hq);
     switch (D) {
       case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
       case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
@@ -546,7 +552,6 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
 
 }  // namespace
 
-int fwd_block_queries() { return 128; }
 
 hipError_t launch_fwd(int dtype, int D, const FwdArgs& a, hipStream_t st) {
   switch (dtype) {
