@@ -164,7 +164,7 @@ def run_main(args):
                             torch)
     achieved = f_fwd / (kern_ms * 1e-3) / 1e12
     workload = "H16_D128_S131072_fp16"
-    roof = {"kernel": "fwd2_kernel<f16,128>", "bound": "mfma", "achieved": round(achieved, 2),
+    roof = {"kernel": "fwd2_kernel<f16,128,4 waves,all phases>", "bound": "mfma", "achieved": round(achieved, 2),
             "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic_for("fwd", workload), "avg_ms": round(kern_ms, 4),
             "algorithmic_flops": f_fwd}

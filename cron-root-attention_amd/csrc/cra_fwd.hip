@@ -373,8 +373,10 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
 }
 
 // NW waves of 32 queries share each K/V tile of BN = 64 rows (2 x 32 KB
-// double buffer at D = 128); at least 2 waves per SIMD.
-template <typename T, int D, int NW>
+// double buffer at D = 128); at least 2 waves per SIMD. PH selects the key
+// phases (bit 0 local window, bit 1 global rows) at compile time, so the
+// phase-restricted launches are kernels of their own in a trace.
+template <typename T, int D, int NW, int PH>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
 void fwd2_kernel(FwdArgs a) {
   constexpr int BN = 64;
@@ -408,8 +410,8 @@ void fwd2_kernel(FwdArgs a) {
   const int lo_k = max(0, m0 - W + 1);
   const int hi = min(S, m0 + kBM);
   const int gmax = glob_prefix(hi - 1, W, a.rpb);
-  const int nloc = (a.phases & 1) ? (hi - lo_k + kBN - 1) / kBN : 0;
-  const int ntot = nloc + ((a.phases & 2) ? (gmax + kBN - 1) / kBN : 0);
+  const int nloc = (PH & 1) ? (hi - lo_k + kBN - 1) / kBN : 0;
+  const int ntot = nloc + ((PH & 2) ? (gmax + kBN - 1) / kBN : 0);
 
   // Buffer resources over the rows this workgroup may read (local rows below
   // hi, global rows below gmax): loads past them return zeros. 32-bit
@@ -532,10 +534,18 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
     FwdArgs b = a;
     b.ntiles = (a.S + 32 * kFwdWaves - 1) / (32 * kFwdWaves);
     const dim3 grid(b.ntiles * b.B * b.Hq), block(64 * kFwdWaves);
+    auto go = [&](auto dc) {
+      constexpr int Dc = decltype(dc)::value;
+      switch (a.phases) {
+        case 1: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 1>), grid, block, 0, st, b); break;
+        case 2: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 2>), grid, block, 0, st, b); break;
+        default: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 3>), grid, block, 0, st, b);
+      }
+    };
     switch (D) {
-      case 32: hipLaunchKernelGGL((fwd2_kernel<T, 32, kFwdWaves>), grid, block, 0, st, b); break;
-      case 64: hipLaunchKernelGGL((fwd2_kernel<T, 64, kFwdWaves>), grid, block, 0, st, b); break;
-      case 128: hipLaunchKernelGGL((fwd2_kernel<T, 128, kFwdWaves>), grid, block, 0, st, b); break;
+      case 32: go(std::integral_constant<int, 32>{}); break;
+      case 64: go(std::integral_constant<int, 64>{}); break;
+      case 128: go(std::integral_constant<int, 128>{}); break;
       default: return hipErrorInvalidValue;
     }
   } else {
