@@ -800,7 +800,7 @@ void dq2_kernel(BwdArgs a, int ntiles) {
 // 64 rows of Q and dO stream through LDS with their LSE and Delta. A key row
 // j sees the queries [j, j+W-1] (local) or [first_query(j), S) (global rows),
 // so every mask is a per-key interval.
-template <typename T, int D, int KB, bool MASK>
+template <typename T, int D, int KB, int BQ, bool MASK>
 __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const float* sL,
                                            const float* sDl, const LaneOffs<D>& lo,
                                            const Frag<T> (&kf)[KB][D / 32],
@@ -808,9 +808,9 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
                                            f32x4 (&dka)[D / 16][KB], f32x4 (&dva)[D / 16][KB],
                                            float c2, int g, int ts, const int (&qmin)[KB],
                                            const int (&qmax)[KB]) {
-  using Tile = SwzTile<D, 64>;
+  using Tile = SwzTile<D, BQ>;
 #pragma unroll
-  for (int qs = 0; qs < 2; ++qs) {
+  for (int qs = 0; qs < BQ / 32; ++qs) {
     float p[2][KB][4], ds[2][KB][4];  // [qb2][kb][r]
 #pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2) {
@@ -863,12 +863,14 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
   }
 }
 
-// NW waves of KB key blocks each cover the workgroup's 128 key rows.
-template <typename T, int D, bool GLOB, int NW, int KB>
+// NW waves of KB key blocks each cover the workgroup's 128 key rows; query
+// tiles of BQ rows.
+template <typename T, int D, bool GLOB, int NW, int KB, int BQ>
 __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
-  using Tile = SwzTile<D, 64>;
-  constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = 64;
+  using Tile = SwzTile<D, BQ>;
+  constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = BQ;
   static_assert(kBK == 128, "128 key rows per workgroup");
+  static_assert(BQ == 32 || BQ == 64 || BQ == 128, "query tile rows");
   // Two pipeline stages as separate LDS objects (see fwd2_kernel): Q and dO
   // rows, and their LSE and Delta.
   __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];
@@ -981,12 +983,21 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
                   (uint32_t)((q_hi - 1) * obytes + D * 2));
     Fill::load(dst[0], rq, fq, qbytes, ts, wave);
     Fill::load(dst[1], ro, fo, obytes, ts, wave);
+    // one lane per query row of the tile (lane i of pass c lands at
+    // dsl[.][64 c + i])
     if (wave == 0) {
       const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + bh * S, (uint32_t)(S * 4));
       const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.delta + bh * S, (uint32_t)(S * 4));
-      const int qrow = min(ts + lane, q_hi - 1);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, CRA_LDS(&dsl[0][0]), 4, qrow * 4, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, CRA_LDS(&dsl[1][0]), 4, qrow * 4, 0, 0, 0);
+#pragma unroll
+      for (int c = 0; c < (kBQ + 63) / 64; ++c) {
+        if (kBQ >= 64 || lane < kBQ) {
+          const int qrow = min(ts + 64 * c + lane, q_hi - 1);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, CRA_LDS(&dsl[0][64 * c]), 4, qrow * 4, 0,
+                                                   0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, CRA_LDS(&dsl[1][64 * c]), 4, qrow * 4, 0,
+                                                   0, 0);
+        }
+      }
     }
   };
   if (ntot > 0) load_tile(0, stage0, sld0);
@@ -1009,10 +1020,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
     if (active && t_last >= wq_lo && ts < wq_hi) {
       const bool full = ts >= full_lo && ts + kBQ <= full_hi && ts + kBQ <= q_hi;
       if (full)
-        dkdv2_tile<T, D, KB, false>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g,
+        dkdv2_tile<T, D, KB, BQ, false>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g,
                                     ts, qmin, qmax);
       else
-        dkdv2_tile<T, D, KB, true>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g,
+        dkdv2_tile<T, D, KB, BQ, true>(cur[0], cur[1], csl[0], csl[1], lo, kf, vf, dka, dva, c2, g,
                                    ts, qmin, qmax);
     }
   };
@@ -1086,6 +1097,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
 // of 16 queries measured 27% slower at D = 128).
 constexpr int kDkdvWaves = 8;
 constexpr int kDqWaves = 4;
+// Query rows per dK/dV tile (32 and 128 measured 6% and 3% slower on the
+// local kernel, equal on the global one).
+constexpr int kDkdvGlobBQ = 64;
+constexpr int kDkdvLocalBQ = 64;
 
 template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
@@ -1099,7 +1114,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, 8 / kDqWaves>), dim3(qtiles * a.B * a.Hq),
                        dim3(64 * kDqWaves), 0, st, a, qtiles);
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvWaves, 8 / kDkdvWaves>),
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvWaves, 8 / kDkdvWaves, kDkdvGlobBQ>),
                        dim3(gtiles * a.nchunk * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a,
                        gtiles);
   } else {
@@ -1110,7 +1125,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   if (a.dalpha && a.relay)
     hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvWaves, 8 / kDkdvWaves>),
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvWaves, 8 / kDkdvWaves, kDkdvLocalBQ>),
                        dim3(ktiles * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a, ktiles);
   else
     hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st,
