@@ -55,6 +55,30 @@ class CraTensor(ctypes.Structure):
                 ("ss", ctypes.c_int64)]
 
 
+class CraDocs(ctypes.Structure):
+    _fields_ = [("n_docs", ctypes.c_int32), ("cu_seqlens", ctypes.POINTER(ctypes.c_int32)),
+                ("window", ctypes.POINTER(ctypes.c_int32)),
+                ("relay", ctypes.POINTER(ctypes.c_int32))]
+
+
+class Docs:
+    """Host-side document table of a varlen call (keeps the int32 arrays alive)."""
+
+    def __init__(self, cu_seqlens, window, relay):
+        n = len(cu_seqlens) - 1
+        self._cu = (ctypes.c_int32 * (n + 1))(*cu_seqlens)
+        self._w = (ctypes.c_int32 * n)(*window)
+        self._r = (ctypes.c_int32 * n)(*(int(x) for x in relay))
+        self.cu_seqlens = list(cu_seqlens)
+        self.window = list(window)
+        self.relay = [bool(x) for x in relay]
+        self.struct = CraDocs(n, self._cu, self._w, self._r)
+
+    @property
+    def n_docs(self) -> int:
+        return len(self.window)
+
+
 class CraDeviceInfo(ctypes.Structure):
     _fields_ = [("cu_count", ctypes.c_int32), ("lds_bytes_per_cu", ctypes.c_int32),
                 ("arch_major", ctypes.c_int32), ("arch_minor", ctypes.c_int32),
@@ -63,6 +87,7 @@ class CraDeviceInfo(ctypes.Structure):
 
 # Exported symbols and their signatures (mirrors include/cra.h).
 _P = ctypes.POINTER(CraProblem)
+_D = ctypes.POINTER(CraDocs)
 _SIGNATURES = {
     "cra_supported_head_dim": (ctypes.c_int, [ctypes.c_int32]),
     "cra_global_rows": (ctypes.c_int64, [_P]),
@@ -78,6 +103,20 @@ _SIGNATURES = {
                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                ctypes.c_void_p, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
                                ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "cra_varlen_sizes": (ctypes.c_int, [_P, _D, ctypes.POINTER(ctypes.c_int64),
+                                        ctypes.POINTER(ctypes.c_int64)]),
+    "cra_build_global_varlen": (ctypes.c_int, [_P, _D, CraTensor, CraTensor, ctypes.c_void_p,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p]),
+    "cra_fwd_varlen": (ctypes.c_int, [_P, _D, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
+                                      ctypes.c_void_p, CraTensor, ctypes.c_void_p,
+                                      ctypes.c_void_p]),
+    "cra_bwd_workspace_bytes_varlen": (ctypes.c_size_t, [_P, _D]),
+    "cra_bwd_varlen": (ctypes.c_int, [_P, _D, CraTensor, CraTensor, CraTensor, CraTensor,
+                                      CraTensor, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "cra_device_info": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(CraDeviceInfo)]),
     "cra_strerror": (ctypes.c_char_p, [ctypes.c_int32]),
     "cra_last_error": (ctypes.c_char_p, []),
@@ -225,6 +264,68 @@ def backward(p: CraProblem, q, k, v, o, do, lse, gk, gv, src, relay_scale, want_
                        tensor_arg(dq), tensor_arg(dk), tensor_arg(dv),
                        dalpha.data_ptr() if dalpha is not None else None, ws.data_ptr(),
                        ws.numel(), _stream(q)), "cra_bwd")
+    return dq, dk, dv, dalpha
+
+
+# ---- varlen: one call over all documents packed along S -------------------
+
+def varlen_sizes(p: CraProblem, docs: Docs):
+    """(packed global rows, relay_src entries) per (b, kv head)."""
+    g, r = ctypes.c_int64(0), ctypes.c_int64(0)
+    _check(load_library().cra_varlen_sizes(ctypes.byref(p), ctypes.byref(docs.struct),
+                                           ctypes.byref(g), ctypes.byref(r)), "cra_varlen_sizes")
+    return int(g.value), int(r.value)
+
+
+def build_global_varlen(p: CraProblem, docs: Docs, k: torch.Tensor, v: torch.Tensor,
+                        relay_scale: Optional[torch.Tensor]):
+    lib = load_library()
+    G, nsrc = varlen_sizes(p, docs)
+    gk = torch.empty(p.B, p.H_kv, G, p.D, dtype=k.dtype, device=k.device)
+    gv = torch.empty_like(gk)
+    src = (torch.empty(p.B, p.H_kv, nsrc, dtype=torch.int32, device=k.device)
+           if nsrc > 0 else None)
+    rs = relay_scale.data_ptr() if (relay_scale is not None and src is not None) else None
+    _check(lib.cra_build_global_varlen(ctypes.byref(p), ctypes.byref(docs.struct), tensor_arg(k),
+                                       tensor_arg(v), gk.data_ptr(), gv.data_ptr(),
+                                       src.data_ptr() if src is not None else None, rs,
+                                       _stream(k)), "cra_build_global_varlen")
+    return gk, gv, src
+
+
+def forward_varlen(p: CraProblem, docs: Docs, q, k, v, gk, gv):
+    lib = load_library()
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(p.B, p.H_q, p.S, dtype=torch.float32, device=q.device)
+    _check(lib.cra_fwd_varlen(ctypes.byref(p), ctypes.byref(docs.struct), tensor_arg(q),
+                              tensor_arg(k), tensor_arg(v), gk.data_ptr(), gv.data_ptr(),
+                              tensor_arg(o), lse.data_ptr(), _stream(q)), "cra_fwd_varlen")
+    return o, lse
+
+
+def workspace_bytes_varlen(p: CraProblem, docs: Docs) -> int:
+    return int(load_library().cra_bwd_workspace_bytes_varlen(ctypes.byref(p),
+                                                             ctypes.byref(docs.struct)))
+
+
+def backward_varlen(p: CraProblem, docs: Docs, q, k, v, o, do, lse, gk, gv, src, relay_scale,
+                    want_dalpha: bool):
+    lib = load_library()
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    nbytes = workspace_bytes_varlen(p, docs)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    dalpha = (torch.empty(p.H_kv, dtype=torch.float32, device=q.device)
+              if (want_dalpha and src is not None) else None)
+    rs = relay_scale.data_ptr() if (relay_scale is not None and src is not None) else None
+    _check(lib.cra_bwd_varlen(ctypes.byref(p), ctypes.byref(docs.struct), tensor_arg(q),
+                              tensor_arg(k), tensor_arg(v), tensor_arg(o), tensor_arg(do),
+                              lse.data_ptr(), gk.data_ptr(), gv.data_ptr(),
+                              src.data_ptr() if src is not None else None, rs, tensor_arg(dq),
+                              tensor_arg(dk), tensor_arg(dv),
+                              dalpha.data_ptr() if dalpha is not None else None, ws.data_ptr(),
+                              ws.numel(), _stream(q)), "cra_bwd_varlen")
     return dq, dk, dv, dalpha
 
 

@@ -209,6 +209,75 @@ def _attention_with_plan(q, k, v, window: int, relay: bool, kv_groups: int = 1,
                                               relay_top_k, window, relay)
 
 
+def _parse_cu_seqlens(cu_seqlens, S_total: int):
+    if isinstance(cu_seqlens, torch.Tensor):
+        if cu_seqlens.device.type != "cpu":
+            raise ValueError("cu_seqlens must be a CPU tensor (or list); call .cpu() first")
+        seqs = [int(x) for x in cu_seqlens.tolist()]
+    else:
+        seqs = [int(x) for x in cu_seqlens]
+    if len(seqs) < 2 or seqs[0] != 0 or seqs[-1] != S_total or any(
+            b <= a for a, b in zip(seqs, seqs[1:])):
+        raise ValueError(f"cu_seqlens must rise strictly from 0 to {S_total}, got {seqs}")
+    return seqs
+
+
+class CronRootAttentionVarlenFunction(torch.autograd.Function):
+    """Autograd of the packed-document op: every document in one set of launches.
+
+    Each document gets the plan of its own length (window ceil(sqrt(len)),
+    relay for len > 2048), exactly what the reference's per-document calls
+    do (core.py:3911-3952); ``windows`` / ``relays`` override the plan per
+    document (test hook).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, seqs, kv_groups: int = 1,
+                relay_log_scale: Optional[torch.Tensor] = None, relay_top_k: int = 2,
+                windows: Optional[Sequence[int]] = None, relays: Optional[Sequence[bool]] = None):
+        _check_inputs(q, k, v, kv_groups)
+        B, Hq, S, D = q.shape
+        Hkv = k.shape[1]
+        lens = [e - s for s, e in zip(seqs, seqs[1:])]
+        W = [window_size(n) for n in lens] if windows is None else [int(w) for w in windows]
+        R = [n > RELAY_THRESHOLD for n in lens] if relays is None else [bool(r) for r in relays]
+        any_relay = any(R)
+        if any_relay and not 1 <= relay_top_k <= 4:
+            raise ValueError(f"relay_top_k={relay_top_k} outside [1, 4]")
+        docs = _native.Docs(seqs, W, R)
+        Dp = _padded_head_dim(D)
+        qp, kp, vp = (_kernel_ready(_pad_d(t, Dp)) for t in (q, k, v))
+        p = _native.problem(B, Hq, Hkv, S, Dp, 0, any_relay, relay_top_k, q.dtype,
+                            1.0 / math.sqrt(D))
+        rscale = None
+        if relay_log_scale is not None and any_relay:
+            if relay_log_scale.shape != (Hkv,):
+                raise ValueError(f"relay_log_scale must have shape [{Hkv}]")
+            rscale = relay_log_scale.detach().exp().to(q.dtype).to(torch.float32).contiguous()
+        gk, gv, src = _native.build_global_varlen(p, docs, kp, vp, rscale)
+        o, lse = _native.forward_varlen(p, docs, qp, kp, vp, gk, gv)
+        ctx.problem = p
+        ctx.docs = docs
+        ctx.D = D
+        ctx.has_alpha = relay_log_scale is not None and any_relay
+        ctx.alpha_dtype = relay_log_scale.dtype if relay_log_scale is not None else None
+        ctx.save_for_backward(qp, kp, vp, o, lse, gk, gv, src, rscale)
+        return o if Dp == D else o[..., :D].contiguous()
+
+    @staticmethod
+    def backward(ctx, do):
+        qp, kp, vp, o, lse, gk, gv, src, rscale = ctx.saved_tensors
+        p = ctx.problem
+        D = ctx.D
+        dop = _kernel_ready(_pad_d(do.to(qp.dtype), p.D))
+        dq, dk, dv, dalpha = _native.backward_varlen(p, ctx.docs, qp, kp, vp, o, dop, lse, gk, gv,
+                                                     src, rscale, ctx.has_alpha)
+        if p.D != D:
+            dq, dk, dv = (t[..., :D].contiguous() for t in (dq, dk, dv))
+        da = dalpha.to(ctx.alpha_dtype) if (ctx.has_alpha and dalpha is not None) else None
+        return dq, dk, dv, None, None, da, None, None, None
+
+
 @torch.compiler.disable
 def cron_root_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                cu_seqlens: Union[Sequence[int], torch.Tensor],
@@ -219,28 +288,26 @@ def cron_root_attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
 
     ``cu_seqlens`` (list or CPU tensor, length n_docs + 1, from 0 to S_total)
     splits the sequence axis; each document is attended on its own with the
-    window and relay rule of its own length.  Documents are zero-copy views
-    (``narrow``); the per-document results are written into one output.
+    window and relay rule of its own length, as the reference's loop of one
+    call per document does.  Here all documents go through one set of kernel
+    launches (``cra_*_varlen``); differentiable, including
+    ``relay_log_scale`` (summed over documents).  ``use_persistent`` has no
+    numerical effect, as in ``cron_root_attention_v14``.
     """
-    if isinstance(cu_seqlens, torch.Tensor):
-        if cu_seqlens.device.type != "cpu":
-            raise ValueError("cu_seqlens must be a CPU tensor (or list); call .cpu() first")
-        seqs = [int(x) for x in cu_seqlens.tolist()]
-    else:
-        seqs = [int(x) for x in cu_seqlens]
-    S_total = q.shape[2]
-    if len(seqs) < 2 or seqs[0] != 0 or seqs[-1] != S_total or any(
-            b <= a for a, b in zip(seqs, seqs[1:])):
-        raise ValueError(f"cu_seqlens must rise strictly from 0 to {S_total}, got {seqs}")
-    if len(seqs) == 2:
+    seqs = _parse_cu_seqlens(cu_seqlens, q.shape[2])
+    if len(seqs) == 2:  # single document: the plain op (core.py:3913-3921)
         return cron_root_attention_v14(q, k, v, use_persistent, kv_groups, relay_log_scale,
                                        relay_top_k)
-    parts = []
-    for s, e in zip(seqs, seqs[1:]):
-        parts.append(cron_root_attention_v14(q.narrow(2, s, e - s), k.narrow(2, s, e - s),
-                                             v.narrow(2, s, e - s), use_persistent, kv_groups,
-                                             relay_log_scale, relay_top_k))
-    return torch.cat(parts, dim=2)
+    return CronRootAttentionVarlenFunction.apply(q, k, v, seqs, kv_groups, relay_log_scale,
+                                                 relay_top_k)
+
+
+def _varlen_with_plan(q, k, v, cu_seqlens, windows, relays, kv_groups: int = 1,
+                      relay_log_scale=None, relay_top_k: int = 2):
+    """Varlen op with explicit per-document windows and relay switches (test hook)."""
+    seqs = _parse_cu_seqlens(cu_seqlens, q.shape[2])
+    return CronRootAttentionVarlenFunction.apply(q, k, v, seqs, kv_groups, relay_log_scale,
+                                                 relay_top_k, windows, relays)
 
 
 def warmup_varlen_shapes(doc_lengths, H: int, D: int, B: int = 1, kv_groups: int = 1,

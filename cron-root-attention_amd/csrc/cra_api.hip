@@ -5,6 +5,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 #include "../../include/cra.h"
 #include "cra_common.hpp"
 #include "cra_internal.hpp"
@@ -28,7 +31,9 @@ int hip_fail(hipError_t e, const char* where) {
 
 int elem_size(int dtype) { return dtype == CRA_F32 ? 4 : 2; }
 
-int check_problem(const cra_problem* p) {
+// Fields every entry point needs; W and relay are checked by the plain
+// entry points only (a varlen call gives them per document).
+int check_problem_common(const cra_problem* p) {
   if (!p) return fail(CRA_E_INVALID, "problem is NULL");
   if (p->dtype != CRA_F16 && p->dtype != CRA_BF16 && p->dtype != CRA_F32)
     return fail(CRA_E_DTYPE, "unknown dtype code %d", p->dtype);
@@ -39,15 +44,25 @@ int check_problem(const cra_problem* p) {
     return fail(CRA_E_INVALID, "H_q (%d) must be a multiple of H_kv (%d)", p->H_q, p->H_kv);
   if (!cra_supported_head_dim(p->D))
     return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128)", p->D);
-  if (p->W < 1 || p->W > p->S)
-    return fail(CRA_E_INVALID, "window W=%d outside [1, S=%d]", p->W, p->S);
-  if (p->relay != 0 && p->relay != 1) return fail(CRA_E_INVALID, "relay must be 0 or 1");
-  if (p->relay && (p->top_k < 1 || p->top_k > 4))
-    return fail(CRA_E_INVALID, "top_k=%d outside [1, 4]", p->top_k);
   if (!(p->scale > 0.f)) return fail(CRA_E_INVALID, "scale must be > 0");
   // 32-bit row indices inside the kernels
   if ((int64_t)p->B * p->H_q * (int64_t)p->S > (int64_t)1 << 31)
     return fail(CRA_E_INVALID, "B*H*S exceeds 2^31");
+  return CRA_OK;
+}
+
+int check_top_k(const cra_problem* p) {
+  if (p->top_k < 1 || p->top_k > 4) return fail(CRA_E_INVALID, "top_k=%d outside [1, 4]", p->top_k);
+  return CRA_OK;
+}
+
+int check_problem(const cra_problem* p) {
+  if (int e = check_problem_common(p)) return e;
+  if (p->W < 1 || p->W > p->S)
+    return fail(CRA_E_INVALID, "window W=%d outside [1, S=%d]", p->W, p->S);
+  if (p->relay != 0 && p->relay != 1) return fail(CRA_E_INVALID, "relay must be 0 or 1");
+  if (p->relay)
+    if (int e = check_top_k(p)) return e;
   return CRA_OK;
 }
 
@@ -81,28 +96,118 @@ int check_buf(const char* name, const void* p) {
 int64_t num_blocks(const cra_problem* p) { return (p->S + p->W - 1) / p->W; }
 int rows_per_block(const cra_problem* p) { return p->relay ? 1 + p->top_k : 1; }
 
-}  // namespace
+// The documents of one call in layout order (a plain call is one document),
+// their packed global rows (gofs) and W-blocks (bofs) per (b, kv head), and
+// the order the kernels take them in: longest first, so that the heaviest
+// work items start first and short documents fill the tail.
+struct Plan {
+  int n = 0;
+  std::vector<int> off, len, W, rpb, gofs, bofs, order;
+  int64_t G = 0;   // packed global rows per (b, kv head)
+  int64_t NB = 0;  // W-blocks per (b, kv head)
+  bool any_relay = false;
+  int top_k = 0;   // relay rows per block of the documents with relay
+};
 
-extern "C" {
-
-int cra_supported_head_dim(int32_t D) { return D == 32 || D == 64 || D == 128; }
-
-int32_t cra_abi_version(void) { return CRA_ABI_VERSION; }
-
-int64_t cra_global_rows(const cra_problem* p) {
-  if (check_problem(p)) return -1;
-  return num_blocks(p) * rows_per_block(p);
+void plan_add(Plan& pl, int off, int len, int W, bool relay, int top_k) {
+  const int nb = (len + W - 1) / W;
+  const int rpb = relay ? 1 + top_k : 1;
+  pl.off.push_back(off);
+  pl.len.push_back(len);
+  pl.W.push_back(W);
+  pl.rpb.push_back(rpb);
+  pl.gofs.push_back((int)pl.G);
+  pl.bofs.push_back((int)pl.NB);
+  pl.G += (int64_t)nb * rpb;
+  pl.NB += nb;
+  pl.any_relay = pl.any_relay || relay;
+  ++pl.n;
 }
 
-int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glob_k, void* glob_v,
-                     int32_t* relay_src, const float* relay_scale, void* stream) {
+void plan_order(Plan& pl) {
+  pl.order.resize(pl.n);
+  for (int d = 0; d < pl.n; ++d) pl.order[d] = d;
+  std::stable_sort(pl.order.begin(), pl.order.end(),
+                   [&](int x, int y) { return pl.len[x] > pl.len[y]; });
+}
+
+int plan_plain(const cra_problem* p, Plan* pl) {
   if (int e = check_problem(p)) return e;
+  *pl = Plan{};
+  pl->top_k = p->relay ? p->top_k : 0;
+  plan_add(*pl, 0, p->S, p->W, p->relay != 0, pl->top_k);
+  plan_order(*pl);
+  return CRA_OK;
+}
+
+int plan_varlen(const cra_problem* p, const cra_docs* d, Plan* pl) {
+  if (int e = check_problem_common(p)) return e;
+  if (!d) return fail(CRA_E_INVALID, "docs is NULL");
+  if (d->n_docs < 1) return fail(CRA_E_INVALID, "n_docs=%d must be >= 1", d->n_docs);
+  if (!d->cu_seqlens || !d->window || !d->relay)
+    return fail(CRA_E_INVALID, "docs: cu_seqlens, window and relay must not be NULL");
+  if (d->cu_seqlens[0] != 0 || d->cu_seqlens[d->n_docs] != p->S)
+    return fail(CRA_E_INVALID, "cu_seqlens must run from 0 to S=%d (got %d .. %d)", p->S,
+                d->cu_seqlens[0], d->cu_seqlens[d->n_docs]);
+  bool relay = false;
+  for (int i = 0; i < d->n_docs; ++i) {
+    const int len = d->cu_seqlens[i + 1] - d->cu_seqlens[i];
+    if (len < 1) return fail(CRA_E_INVALID, "cu_seqlens must rise strictly (document %d)", i);
+    if (d->window[i] < 1 || d->window[i] > len)
+      return fail(CRA_E_INVALID, "document %d: window %d outside [1, %d]", i, d->window[i], len);
+    if (d->relay[i] != 0 && d->relay[i] != 1)
+      return fail(CRA_E_INVALID, "document %d: relay must be 0 or 1", i);
+    relay = relay || d->relay[i];
+  }
+  if (relay)
+    if (int e = check_top_k(p)) return e;
+  *pl = Plan{};
+  pl->top_k = relay ? p->top_k : 0;
+  for (int i = 0; i < d->n_docs; ++i)
+    plan_add(*pl, d->cu_seqlens[i], d->cu_seqlens[i + 1] - d->cu_seqlens[i], d->window[i],
+             d->relay[i] != 0, pl->top_k);
+  if (pl->G * p->D >= ((int64_t)1 << 31))
+    return fail(CRA_E_INVALID, "%lld packed global rows per head exceed the 32-bit offsets",
+                (long long)pl->G);
+  plan_order(*pl);
+  return CRA_OK;
+}
+
+int num_groups(const Plan& pl) { return (pl.n + cra::kMaxDocs - 1) / cra::kMaxDocs; }
+
+// Kernel-argument table of document group g (up to kMaxDocs documents, in
+// launch order); the launchers number the work items.
+cra::Docs group_table(const Plan& pl, int g) {
+  cra::Docs t{};
+  const int lo = g * cra::kMaxDocs;
+  t.n = std::min(pl.n - lo, cra::kMaxDocs);
+  for (int i = 0; i < t.n; ++i) {
+    const int d = pl.order[lo + i];
+    t.off[i] = pl.off[d];
+    t.len[i] = pl.len[d];
+    t.W[i] = pl.W[d];
+    t.rpb[i] = pl.rpb[d];
+    t.gofs[i] = pl.gofs[d];
+    t.bofs[i] = pl.bofs[d];
+  }
+  return t;
+}
+
+size_t workspace_bytes(const cra_problem* p, const Plan& pl, int* nchunk) {
+  return cra::bwd_workspace_bytes(p->D, p->B, p->H_q, p->H_kv, p->S, pl.n, pl.len.data(),
+                                  pl.W.data(), pl.rpb.data(), pl.G, nchunk);
+}
+
+int build_global_impl(const cra_problem* p, const Plan& pl, cra_tensor k, cra_tensor v,
+                      void* glob_k, void* glob_v, int32_t* relay_src, const float* relay_scale,
+                      void* stream) {
   const int esz = elem_size(p->dtype);
   if (int e = check_tensor("k", k, esz)) return e;
   if (int e = check_tensor("v", v, esz)) return e;
   if (int e = check_buf("glob_k", glob_k)) return e;
   if (int e = check_buf("glob_v", glob_v)) return e;
-  if (p->relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
+  if (pl.any_relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
+  if ((int64_t)p->B * p->H_kv > 65535) return fail(CRA_E_INVALID, "B*H_kv exceeds 65535");
   cra::GlobalArgs a{};
   a.k = k.ptr;
   a.v = v.ptr;
@@ -113,29 +218,20 @@ int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glo
   a.src = relay_src;
   a.scale = relay_scale;
   a.Hkv = p->H_kv;
-  a.S = p->S;
-  a.W = p->W;
-  a.NB = (int)num_blocks(p);
-  a.rpb = rows_per_block(p);
-  a.top_k = p->relay ? p->top_k : 0;
-  a.relay = p->relay;
-  a.G = num_blocks(p) * a.rpb;
-  if ((int64_t)p->B * p->H_kv > 65535) return fail(CRA_E_INVALID, "B*H_kv exceeds 65535");
-  hipError_t e = cra::launch_build_global(p->dtype, p->D, a, p->B, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "cra_build_global launch");
+  a.top_k = pl.top_k;
+  a.NB = (int)pl.NB;
+  a.G = pl.G;
+  for (int g = 0; g < num_groups(pl); ++g) {
+    a.docs = group_table(pl, g);
+    hipError_t e = cra::launch_build_global(p->dtype, p->D, a, p->B, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "cra_build_global launch");
+  }
   return CRA_OK;
 }
 
-int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, const void* glob_k,
-            const void* glob_v, cra_tensor o, float* lse, void* stream) {
-  return cra_fwd_phases(p, q, k, v, glob_k, glob_v, o, lse, CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL,
-                        stream);
-}
-
-int cra_fwd_phases(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
-                   const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
-                   int32_t phase_mask, void* stream) {
-  if (int e = check_problem(p)) return e;
+int fwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, cra_tensor v,
+             const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+             int32_t phase_mask, void* stream) {
   if (phase_mask < 1 || phase_mask > (CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL))
     return fail(CRA_E_INVALID, "phase_mask must be a non-empty subset of CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL");
   const int esz = elem_size(p->dtype);
@@ -154,29 +250,23 @@ int cra_fwd_phases(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor 
   a.ksb = k.sb; a.ksh = k.sh; a.kss = k.ss;
   a.vsb = v.sb; a.vsh = v.sh; a.vss = v.ss;
   a.osb = o.sb; a.osh = o.sh; a.oss = o.ss;
-  a.B = p->B; a.Hq = p->H_q; a.Hkv = p->H_kv; a.S = p->S; a.W = p->W;
-  a.rpb = rows_per_block(p);
-  a.G = num_blocks(p) * a.rpb;
+  a.B = p->B; a.Hq = p->H_q; a.Hkv = p->H_kv; a.S = p->S;
+  a.G = pl.G;
   a.scale = p->scale;
-  a.ntiles = (p->S + 127) / 128;
   a.phases = phase_mask;
-  hipError_t e = cra::launch_fwd(p->dtype, p->D, a, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "cra_fwd launch");
+  for (int g = 0; g < num_groups(pl); ++g) {
+    a.docs = group_table(pl, g);
+    hipError_t e = cra::launch_fwd(p->dtype, p->D, a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "cra_fwd launch");
+  }
   return CRA_OK;
 }
 
-size_t cra_bwd_workspace_bytes(const cra_problem* p) {
-  if (check_problem(p)) return 0;
-  int nchunk = 0, chunk_len = 0;
-  return cra::bwd_workspace_bytes(p->D, p->B, p->H_q, p->H_kv, p->S, p->W,
-                                  num_blocks(p) * rows_per_block(p), &nchunk, &chunk_len);
-}
-
-int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
-            cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
-            const int32_t* relay_src, const float* relay_scale, cra_tensor dq, cra_tensor dk,
-            cra_tensor dv, float* dalpha, void* workspace, size_t workspace_bytes, void* stream) {
-  if (int e = check_problem(p)) return e;
+int bwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, cra_tensor v,
+             cra_tensor o, cra_tensor dout, const float* lse, const void* glob_k,
+             const void* glob_v, const int32_t* relay_src, const float* relay_scale,
+             cra_tensor dq, cra_tensor dk, cra_tensor dv, float* dalpha, void* workspace,
+             size_t workspace_bytes_given, void* stream) {
   const int esz = elem_size(p->dtype);
   if (int e = check_tensor("q", q, esz)) return e;
   if (int e = check_tensor("k", k, esz)) return e;
@@ -194,14 +284,12 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
   if (int e = check_buf("lse", lse)) return e;
   if (int e = check_buf("glob_k", glob_k)) return e;
   if (int e = check_buf("glob_v", glob_v)) return e;
-  if (p->relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
-  const int64_t G = num_blocks(p) * rows_per_block(p);
-  int nchunk = 0, chunk_len = 0;
-  const size_t need = cra::bwd_workspace_bytes(p->D, p->B, p->H_q, p->H_kv, p->S, p->W, G,
-                                               &nchunk, &chunk_len);
-  if (need > 0 && (!workspace || workspace_bytes < need))
+  if (pl.any_relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
+  int nchunk = 0;
+  const size_t need = workspace_bytes(p, pl, &nchunk);
+  if (need > 0 && (!workspace || workspace_bytes_given < need))
     return fail(CRA_E_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
-                workspace ? workspace_bytes : (size_t)0);
+                workspace ? workspace_bytes_given : (size_t)0);
   if (workspace && reinterpret_cast<uintptr_t>(workspace) % 256)
     return fail(CRA_E_LAYOUT, "workspace not 256-byte aligned");
   cra::BwdArgs a{};
@@ -216,23 +304,120 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
   a.dqsb = dq.sb; a.dqsh = dq.sh; a.dqss = dq.ss;
   a.dksb = dk.sb; a.dksh = dk.sh; a.dkss = dk.ss;
   a.dvsb = dv.sb; a.dvsh = dv.sh; a.dvss = dv.ss;
-  a.B = p->B; a.Hq = p->H_q; a.Hkv = p->H_kv; a.S = p->S; a.W = p->W;
-  a.rpb = rows_per_block(p);
-  a.top_k = p->relay ? p->top_k : 0;
-  a.relay = p->relay;
-  a.G = G;
+  a.B = p->B; a.Hq = p->H_q; a.Hkv = p->H_kv; a.S = p->S;
+  a.top_k = pl.top_k;
+  a.NB = (int)pl.NB;
+  a.G = pl.G;
   a.scale = p->scale;
   a.nchunk = nchunk;
-  a.chunk_len = chunk_len;
   // workspace carve-up: delta [B*Hq*S] fp32, then the global-row partials
   char* ws = static_cast<char*>(workspace);
   const size_t delta_bytes = (((size_t)p->B * p->H_q * p->S * 4) + 255) / 256 * 256;
   a.delta = reinterpret_cast<float*>(ws);
   a.gpart = reinterpret_cast<float*>(ws + delta_bytes);
   a.dalpha = dalpha;
-  hipError_t e = cra::launch_bwd(p->dtype, p->D, a, (hipStream_t)stream);
-  if (e != hipSuccess) return hip_fail(e, "cra_bwd launch");
+  for (int g = 0; g < num_groups(pl); ++g) {
+    a.group = g;
+    a.docs = group_table(pl, g);
+    hipError_t e = cra::launch_bwd(p->dtype, p->D, a, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "cra_bwd launch");
+  }
   return CRA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cra_supported_head_dim(int32_t D) { return D == 32 || D == 64 || D == 128; }
+
+int32_t cra_abi_version(void) { return CRA_ABI_VERSION; }
+
+int64_t cra_global_rows(const cra_problem* p) {
+  if (check_problem(p)) return -1;
+  return num_blocks(p) * rows_per_block(p);
+}
+
+int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glob_k, void* glob_v,
+                     int32_t* relay_src, const float* relay_scale, void* stream) {
+  Plan pl;
+  if (int e = plan_plain(p, &pl)) return e;
+  return build_global_impl(p, pl, k, v, glob_k, glob_v, relay_src, relay_scale, stream);
+}
+
+int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, const void* glob_k,
+            const void* glob_v, cra_tensor o, float* lse, void* stream) {
+  return cra_fwd_phases(p, q, k, v, glob_k, glob_v, o, lse, CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL,
+                        stream);
+}
+
+int cra_fwd_phases(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+                   const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                   int32_t phase_mask, void* stream) {
+  Plan pl;
+  if (int e = plan_plain(p, &pl)) return e;
+  return fwd_impl(p, pl, q, k, v, glob_k, glob_v, o, lse, phase_mask, stream);
+}
+
+size_t cra_bwd_workspace_bytes(const cra_problem* p) {
+  Plan pl;
+  if (plan_plain(p, &pl)) return 0;
+  int nchunk = 0;
+  return workspace_bytes(p, pl, &nchunk);
+}
+
+int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+            cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
+            const int32_t* relay_src, const float* relay_scale, cra_tensor dq, cra_tensor dk,
+            cra_tensor dv, float* dalpha, void* workspace, size_t workspace_bytes, void* stream) {
+  Plan pl;
+  if (int e = plan_plain(p, &pl)) return e;
+  return bwd_impl(p, pl, q, k, v, o, dout, lse, glob_k, glob_v, relay_src, relay_scale, dq, dk,
+                  dv, dalpha, workspace, workspace_bytes, stream);
+}
+
+int cra_varlen_sizes(const cra_problem* p, const cra_docs* docs, int64_t* global_rows,
+                     int64_t* relay_src_len) {
+  Plan pl;
+  if (int e = plan_varlen(p, docs, &pl)) return e;
+  if (global_rows) *global_rows = pl.G;
+  if (relay_src_len) *relay_src_len = pl.NB * pl.top_k;
+  return CRA_OK;
+}
+
+int cra_build_global_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor k,
+                            cra_tensor v, void* glob_k, void* glob_v, int32_t* relay_src,
+                            const float* relay_scale, void* stream) {
+  Plan pl;
+  if (int e = plan_varlen(p, docs, &pl)) return e;
+  return build_global_impl(p, pl, k, v, glob_k, glob_v, relay_src, relay_scale, stream);
+}
+
+int cra_fwd_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor q, cra_tensor k,
+                   cra_tensor v, const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                   void* stream) {
+  Plan pl;
+  if (int e = plan_varlen(p, docs, &pl)) return e;
+  return fwd_impl(p, pl, q, k, v, glob_k, glob_v, o, lse, CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL,
+                  stream);
+}
+
+size_t cra_bwd_workspace_bytes_varlen(const cra_problem* p, const cra_docs* docs) {
+  Plan pl;
+  if (plan_varlen(p, docs, &pl)) return 0;
+  int nchunk = 0;
+  return workspace_bytes(p, pl, &nchunk);
+}
+
+int cra_bwd_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor q, cra_tensor k,
+                   cra_tensor v, cra_tensor o, cra_tensor dout, const float* lse,
+                   const void* glob_k, const void* glob_v, const int32_t* relay_src,
+                   const float* relay_scale, cra_tensor dq, cra_tensor dk, cra_tensor dv,
+                   float* dalpha, void* workspace, size_t workspace_bytes, void* stream) {
+  Plan pl;
+  if (int e = plan_varlen(p, docs, &pl)) return e;
+  return bwd_impl(p, pl, q, k, v, o, dout, lse, glob_k, glob_v, relay_src, relay_scale, dq, dk,
+                  dv, dalpha, workspace, workspace_bytes, stream);
 }
 
 int cra_device_info(int32_t device, cra_device_info_t* out) {

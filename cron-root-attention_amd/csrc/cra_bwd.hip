@@ -158,7 +158,7 @@ __device__ __forceinline__ void dq_tile(const T* sK, const T* sV, const T* sKt,
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void dq_kernel(BwdArgs a, int ntiles) {
+__global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
   using Tr = BwdTraits<T, D>;
   __shared__ __attribute__((aligned(16))) T sK[Tr::kBN * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sV[Tr::kBN * Tr::kLD];
@@ -169,18 +169,22 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a, int ntiles) {
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hq;
   const int bh = blockIdx.x % nbh;
-  const int tile = ntiles - 1 - (int)(blockIdx.x / nbh);
+  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  const int tile = (dc.len + Tr::kBM - 1) / Tr::kBM - 1 - dc.item;  // heaviest first
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int m0 = tile * Tr::kBM;
   const int q0 = m0 + wave * Tr::kQW;
-  const int S = a.S, W = a.W;
+  const int S = dc.len, W = dc.W, rpb = dc.rpb;
 
-  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
-  const T* dop = static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh;
-  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
-  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh + (int64_t)dc.off * a.qss;
+  const T* dop =
+      static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh + (int64_t)dc.off * a.doss;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
+  const float* lse = a.lse + (int64_t)bh * a.S + dc.off;
+  const float* delta = a.delta + (int64_t)bh * a.S + dc.off;
+  const int64_t gbase = ((int64_t)(b * a.Hkv + hk) * a.G + dc.gofs) * D;
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
 
@@ -191,8 +195,8 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a, int ntiles) {
   for (int qb = 0; qb < 2; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
     const bool ok = qi[qb] < S;
-    lse2[qb] = ok ? a.lse[(int64_t)bh * S + qi[qb]] * kLog2e : 0.f;
-    dl[qb] = ok ? a.delta[(int64_t)bh * S + qi[qb]] : 0.f;
+    lse2[qb] = ok ? lse[qi[qb]] * kLog2e : 0.f;
+    dl[qb] = ok ? delta[qi[qb]] : 0.f;
 #pragma unroll
     for (int c = 0; c < Tr::kDC; ++c) {
       if (ok) {
@@ -237,10 +241,10 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a, int ntiles) {
     }
   }
 
-  const int gmax = glob_prefix(hi - 1, W, a.rpb);
-  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
-  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
-  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+  const int gmax = glob_prefix(hi - 1, W, rpb);
+  const int wg_lo = active ? glob_prefix(q0, W, rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, rpb), glob_prefix(qi[1], W, rpb)};
   for (int ts = 0; ts < gmax; ts += Tr::kBN) {
     stk.load(gkp, D, ts, 0, gmax, tid);
     stv.load(gvp, D, ts, 0, gmax, tid);
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a, int ntiles) {
     }
   }
 
-  T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;
+  T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh + (int64_t)dc.off * a.dqss;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     if (!active || qi[qb] >= S) continue;
@@ -352,7 +356,7 @@ __device__ __forceinline__ void dkdv_tile(const T* sQ, const T* sO, const T* sQt
 }
 
 template <typename T, int D, bool GLOB>
-__global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
+__global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
   using Tr = BwdTraits<T, D>;
   __shared__ __attribute__((aligned(16))) T sQ[Tr::kBQ * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sO[Tr::kBQ * Tr::kLD];
@@ -368,12 +372,14 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
   const int nbh = a.B * a.Hkv;
   const int bhk = blockIdx.x % nbh;
   const int rest = blockIdx.x / nbh;
-  const int chunk = GLOB ? rest % a.nchunk : 0;
-  const int tile = GLOB ? rest / a.nchunk : rest;
+  const Doc dc = find_doc(a.docs, rest);
+  const int chunk = GLOB ? dc.item % a.nchunk : 0;
+  const int tile = GLOB ? dc.item / a.nchunk : dc.item;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int grp = a.Hq / a.Hkv;
-  const int S = a.S, W = a.W;
-  const int nrows = GLOB ? (int)a.G : S;
+  const int S = dc.len, W = dc.W, rpb = dc.rpb;
+  const bool relay = rpb > 1;
+  const int nrows = GLOB ? (S + W - 1) / W * rpb : S;  // keys: global rows or rows
   const int k0 = tile * Tr::kBK;
   const int kw = k0 + wave * Tr::kKW;
 
@@ -381,14 +387,14 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
   const T* vbase;
   int64_t kstride, vstride;
   if (GLOB) {
-    const int64_t gb = (int64_t)bhk * a.G * D;
+    const int64_t gb = ((int64_t)bhk * a.G + dc.gofs) * D;
     kbase = static_cast<const T*>(a.gk) + gb;
     vbase = static_cast<const T*>(a.gv) + gb;
     kstride = D;
     vstride = D;
   } else {
-    kbase = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-    vbase = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+    kbase = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
+    vbase = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
     kstride = a.kss;
     vstride = a.vss;
   }
@@ -418,11 +424,12 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
   const bool active = kw < nrows;
   int q_lo, q_hi, wq_lo, wq_hi;
   if (GLOB) {
-    const int c_lo = chunk * a.chunk_len;
-    const int c_hi = min(S, c_lo + a.chunk_len);
-    q_lo = max(c_lo, glob_row_first_query(k0, W, a.rpb));
+    const int chunk_len = chunk_len_for(S, a.nchunk);
+    const int c_lo = chunk * chunk_len;
+    const int c_hi = min(S, c_lo + chunk_len);
+    q_lo = max(c_lo, glob_row_first_query(k0, W, rpb));
     q_hi = c_hi;
-    wq_lo = active ? max(c_lo, glob_row_first_query(kw, W, a.rpb)) : S;
+    wq_lo = active ? max(c_lo, glob_row_first_query(kw, W, rpb)) : S;
     wq_hi = c_hi;
   } else {
     q_lo = k0;
@@ -437,8 +444,11 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
   for (int j = 0; j < grp; ++j) {
     const int h = hk * grp + j;
     const int bh = b * a.Hq + h;
-    const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
-    const T* dop = static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh;
+    const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh + (int64_t)dc.off * a.qss;
+    const T* dop =
+        static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh + (int64_t)dc.off * a.doss;
+    const float* lse = a.lse + (int64_t)bh * a.S + dc.off;
+    const float* delta = a.delta + (int64_t)bh * a.S + dc.off;
     for (int ts = q_lo; ts < q_hi; ts += Tr::kBQ) {
       stq.load(qp, a.qss, ts, 0, q_hi, tid);
       sto.load(dop, a.doss, ts, 0, q_hi, tid);
@@ -450,16 +460,16 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
       if (tid < Tr::kBQ) {
         const int qabs = ts + tid;
         const bool ok = qabs < q_hi;
-        sL[tid] = ok ? a.lse[(int64_t)bh * S + qabs] * kLog2e : 0.f;
-        sDl[tid] = ok ? a.delta[(int64_t)bh * S + qabs] : 0.f;
-        if (GLOB) sGl[tid] = ok ? glob_prefix(qabs, W, a.rpb) : 0;
+        sL[tid] = ok ? lse[qabs] * kLog2e : 0.f;
+        sDl[tid] = ok ? delta[qabs] : 0.f;
+        if (GLOB) sGl[tid] = ok ? glob_prefix(qabs, W, rpb) : 0;
       }
       __syncthreads();
       const int t_last = min(ts + Tr::kBQ, q_hi) - 1;
       if (active && t_last >= wq_lo && ts < wq_hi) {
         bool full;
         if (GLOB)
-          full = ts + Tr::kBQ <= q_hi && glob_prefix(ts, W, a.rpb) > k_last;
+          full = ts + Tr::kBQ <= q_hi && glob_prefix(ts, W, rpb) > k_last;
         else
           full = ts >= k_last && ts + Tr::kBQ - 1 - W + 1 <= kw && ts + Tr::kBQ <= q_hi;
         if (full)
@@ -474,7 +484,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
 
   // Epilogue. Lane owns key row kw + 16kb + l16, dims 16db + 4g .. +4.
   if (GLOB) {
-    float* part = a.gpart + ((int64_t)chunk * nbh + bhk) * a.G * 2 * D;
+    float* part = a.gpart + (((int64_t)chunk * nbh + bhk) * a.G + dc.gofs) * 2 * D;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int row = kw + 16 * kb + l16;
@@ -488,9 +498,9 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
     }
     return;
   }
-  T* dkp = static_cast<T*>(a.dk) + b * a.dksb + hk * a.dksh;
-  T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh;
-  const float rsc = (a.relay && a.rscale) ? a.rscale[hk] : 1.f;
+  T* dkp = static_cast<T*>(a.dk) + b * a.dksb + hk * a.dksh + (int64_t)dc.off * a.dkss;
+  T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh + (int64_t)dc.off * a.dvss;
+  const float rsc = (relay && a.rscale) ? a.rscale[hk] : 1.f;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
     const int j = kw + 16 * kb + l16;
@@ -504,21 +514,22 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a, int ntiles) {
     float gsc[5];
     int nm = 0;
     if (j == rblk * W) {
-      grow[nm] = rblk * a.rpb;
+      grow[nm] = rblk * rpb;
       gsc[nm++] = 1.f;
     }
-    if (a.relay) {
-      const int32_t* src = a.src + ((int64_t)bhk * (a.G / a.rpb) + rblk) * a.top_k;
+    if (relay) {
+      const int32_t* src = a.src + ((int64_t)bhk * a.NB + dc.bofs + rblk) * a.top_k;
       for (int t = 0; t < a.top_k; ++t) {
         if (src[t] == j) {
-          grow[nm] = rblk * a.rpb + 1 + t;
+          grow[nm] = rblk * rpb + 1 + t;
           gsc[nm++] = rsc;
         }
       }
     }
     for (int m = 0; m < nm; ++m) {
       for (int c = 0; c < a.nchunk; ++c) {
-        const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + grow[m]) * 2 * D;
+        const float* pk =
+            a.gpart + (((int64_t)c * nbh + bhk) * a.G + dc.gofs + grow[m]) * 2 * D;
 #pragma unroll
         for (int db = 0; db < Tr::kDB; ++db) {
           dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
@@ -543,22 +554,26 @@ __global__ __launch_bounds__(256) void dalpha_kernel(BwdArgs a) {
   const int hk = blockIdx.x;
   const int tid = threadIdx.x;
   const int nbh = a.B * a.Hkv;
-  const int nrel = (int)(a.G / a.rpb) * a.top_k;
   float acc = 0.f;
   for (int b = 0; b < a.B; ++b) {
     const int bhk = b * a.Hkv + hk;
     const T* gk = static_cast<const T*>(a.gk) + (int64_t)bhk * a.G * D;
     const T* gv = static_cast<const T*>(a.gv) + (int64_t)bhk * a.G * D;
-    for (int e = tid; e < nrel * D; e += 256) {
-      const int t = e / D, d = e % D;
-      const int row = (t / a.top_k) * a.rpb + 1 + t % a.top_k;
-      float dk = 0.f, dv = 0.f;
-      for (int c = 0; c < a.nchunk; ++c) {
-        const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + row) * 2 * D;
-        dk += pk[d];
-        dv += pk[D + d];
+    for (int doc = 0; doc < a.docs.n; ++doc) {
+      const int rpb = a.docs.rpb[doc];
+      if (rpb == 1) continue;  // no relay rows in this document
+      const int nrel = (a.docs.len[doc] + a.docs.W[doc] - 1) / a.docs.W[doc] * a.top_k;
+      for (int e = tid; e < nrel * D; e += 256) {
+        const int t = e / D, d = e % D;
+        const int row = a.docs.gofs[doc] + (t / a.top_k) * rpb + 1 + t % a.top_k;
+        float dk = 0.f, dv = 0.f;
+        for (int c = 0; c < a.nchunk; ++c) {
+          const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + row) * 2 * D;
+          dk += pk[d];
+          dv += pk[D + d];
+        }
+        acc += dk * to_f32(gk[(int64_t)row * D + d]) + dv * to_f32(gv[(int64_t)row * D + d]);
       }
-      acc += dk * to_f32(gk[(int64_t)row * D + d]) + dv * to_f32(gv[(int64_t)row * D + d]);
     }
   }
   __shared__ float red[256];
@@ -568,7 +583,7 @@ __global__ __launch_bounds__(256) void dalpha_kernel(BwdArgs a) {
     if (tid < off) red[tid] += red[tid + off];
     __syncthreads();
   }
-  if (tid == 0) a.dalpha[hk] = red[0];
+  if (tid == 0) a.dalpha[hk] = (a.group ? a.dalpha[hk] : 0.f) + red[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -658,7 +673,7 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
 // queries; at least 2 waves per SIMD.
 template <typename T, int D, int NW, int QB>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
-void dq2_kernel(BwdArgs a, int ntiles) {
+void dq2_kernel(BwdArgs a) {
   using Tile = SwzTile<D, 64>;
   constexpr int kQW = 16 * QB, kBM = NW * kQW, kBN = 64;
   static_assert(kBM == 128, "128 queries per workgroup");
@@ -671,24 +686,28 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hq;
   const int bh = blockIdx.x % nbh;
-  const int tile = ntiles - 1 - (int)(blockIdx.x / nbh);
+  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  const int tile = (dc.len + kBM - 1) / kBM - 1 - dc.item;  // heaviest first
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int m0 = tile * kBM;
   const int q0 = m0 + wave * kQW;
-  const int S = a.S, W = a.W;
+  const int S = dc.len, W = dc.W, rpb = dc.rpb;
 
-  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
-  const T* dop = static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh;
-  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
-  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh + (int64_t)dc.off * a.qss;
+  const T* dop =
+      static_cast<const T*>(a.dout) + b * a.dosb + h * a.dosh + (int64_t)dc.off * a.doss;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
+  const float* lse = a.lse + (int64_t)bh * a.S + dc.off;
+  const float* delta = a.delta + (int64_t)bh * a.S + dc.off;
+  const int64_t gbase = ((int64_t)(b * a.Hkv + hk) * a.G + dc.gofs) * D;
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
 
   const int lo_k = max(0, m0 - W + 1);
   const int hi = min(S, m0 + kBM);
-  const int gmax = glob_prefix(hi - 1, W, a.rpb);
+  const int gmax = glob_prefix(hi - 1, W, rpb);
   const int nloc = (hi - lo_k + kBN - 1) / kBN;
   const int ntot = nloc + (gmax + kBN - 1) / kBN;
   // Buffer resources over the rows this workgroup may read (local rows below
@@ -723,8 +742,8 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   for (int qb = 0; qb < QB; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
     const bool ok = qi[qb] < S;
-    lse2[qb] = ok ? a.lse[(int64_t)bh * S + qi[qb]] * kLog2e : 0.f;
-    dl[qb] = ok ? a.delta[(int64_t)bh * S + qi[qb]] : 0.f;
+    lse2[qb] = ok ? lse[qi[qb]] * kLog2e : 0.f;
+    dl[qb] = ok ? delta[qi[qb]] : 0.f;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) {
       if (ok) {
@@ -746,11 +765,11 @@ void dq2_kernel(BwdArgs a, int ntiles) {
   const bool active = q0 < S;
   const int q_last = min(q0 + kQW, S) - 1;
   const int w_lo = max(0, q0 - W + 1);
-  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
-  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
+  const int wg_lo = active ? glob_prefix(q0, W, rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
   int glen[QB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) glen[qb] = glob_prefix(qi[qb], W, a.rpb);
+  for (int qb = 0; qb < QB; ++qb) glen[qb] = glob_prefix(qi[qb], W, rpb);
 
   // Local and global tiles share one body (parameters chosen per tile); the
   // loop is unrolled over the two stages.
@@ -785,7 +804,7 @@ void dq2_kernel(BwdArgs a, int ntiles) {
     if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
   }
 
-  T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh;
+  T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh + (int64_t)dc.off * a.dqss;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     if (!active || qi[qb] >= S) continue;
@@ -866,7 +885,7 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
 // NW waves of KB key blocks each cover the workgroup's 128 key rows; query
 // tiles of BQ rows.
 template <typename T, int D, bool GLOB, int NW, int KB, int BQ>
-__global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
+__global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
   using Tile = SwzTile<D, BQ>;
   constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = BQ;
   static_assert(kBK == 128, "128 key rows per workgroup");
@@ -884,12 +903,14 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
   const int nbh = a.B * a.Hkv;
   const int bhk = blockIdx.x % nbh;
   const int rest = blockIdx.x / nbh;
-  const int chunk = GLOB ? rest % a.nchunk : 0;
-  const int tile = GLOB ? rest / a.nchunk : rest;
+  const Doc dc = find_doc(a.docs, rest);
+  const int chunk = GLOB ? dc.item % a.nchunk : 0;
+  const int tile = GLOB ? dc.item / a.nchunk : dc.item;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int grp = a.Hq / a.Hkv;
-  const int S = a.S, W = a.W;
-  const int nrows = GLOB ? (int)a.G : S;
+  const int S = dc.len, W = dc.W, rpb = dc.rpb;
+  const bool relay = rpb > 1;
+  const int nrows = GLOB ? (S + W - 1) / W * rpb : S;  // keys: global rows or rows
   const int k0 = tile * kBK;
   const int kw = k0 + wave * kKW;
 
@@ -897,14 +918,14 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
   const T* vbase;
   int64_t kstride, vstride;
   if (GLOB) {
-    const int64_t gb = (int64_t)bhk * a.G * D;
+    const int64_t gb = ((int64_t)bhk * a.G + dc.gofs) * D;
     kbase = static_cast<const T*>(a.gk) + gb;
     vbase = static_cast<const T*>(a.gv) + gb;
     kstride = D;
     vstride = D;
   } else {
-    kbase = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-    vbase = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
+    kbase = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
+    vbase = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
     kstride = a.kss;
     vstride = a.vss;
   }
@@ -912,9 +933,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
   // query interval of the workgroup; per-key intervals for the masks
   int q_lo, q_hi;
   if (GLOB) {
-    const int c_lo = chunk * a.chunk_len;
-    q_hi = min(S, c_lo + a.chunk_len);
-    q_lo = max(c_lo, glob_row_first_query(k0, W, a.rpb));
+    const int chunk_len = chunk_len_for(S, a.nchunk);
+    const int c_lo = chunk * chunk_len;
+    q_hi = min(S, c_lo + chunk_len);
+    q_lo = max(c_lo, glob_row_first_query(k0, W, rpb));
   } else {
     q_lo = k0;
     q_hi = min(S, k0 + kBK - 1 + W);
@@ -935,7 +957,7 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
     const int row = kw + 16 * kb + l16;
     // query rows at or past q_hi load as zeros: excluded
     if (GLOB) {
-      qmin[kb] = row < nrows ? glob_row_first_query(row, W, a.rpb) : S;
+      qmin[kb] = row < nrows ? glob_row_first_query(row, W, rpb) : S;
       qmax[kb] = q_hi - 1;
     } else {
       qmin[kb] = row;
@@ -961,9 +983,9 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
   const bool active = kw < nrows;
   const int k_last = min(kw + kKW, nrows) - 1;
   // queries this wave can see at all
-  const int wq_lo = GLOB ? (active ? max(q_lo, glob_row_first_query(kw, W, a.rpb)) : S) : kw;
+  const int wq_lo = GLOB ? (active ? max(q_lo, glob_row_first_query(kw, W, rpb)) : S) : kw;
   const int wq_hi = GLOB ? q_hi : min(q_hi, kw + kKW - 1 + W);
-  const int full_lo = GLOB ? (active ? glob_row_first_query(k_last, W, a.rpb) : S) : k_last;
+  const int full_lo = GLOB ? (active ? glob_row_first_query(k_last, W, rpb) : S) : k_last;
   const int full_hi = GLOB ? q_hi : kw + W;  // exclusive
   const float c2 = a.scale * kLog2e;
 
@@ -975,19 +997,20 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
     const int hq = hk * grp + j;
     const int64_t bh = (int64_t)b * a.Hq + hq;
     // rows at or past q_hi load as zeros
-    const __amdgpu_buffer_rsrc_t rq =
-        make_rsrc(static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh,
-                  (uint32_t)((q_hi - 1) * qbytes + D * 2));
-    const __amdgpu_buffer_rsrc_t ro =
-        make_rsrc(static_cast<const T*>(a.dout) + b * a.dosb + hq * a.dosh,
-                  (uint32_t)((q_hi - 1) * obytes + D * 2));
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh + (int64_t)dc.off * a.qss,
+        (uint32_t)((q_hi - 1) * qbytes + D * 2));
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(
+        static_cast<const T*>(a.dout) + b * a.dosb + hq * a.dosh + (int64_t)dc.off * a.doss,
+        (uint32_t)((q_hi - 1) * obytes + D * 2));
     Fill::load(dst[0], rq, fq, qbytes, ts, wave);
     Fill::load(dst[1], ro, fo, obytes, ts, wave);
     // one lane per query row of the tile (lane i of pass c lands at
     // dsl[.][64 c + i])
     if (wave == 0) {
-      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + bh * S, (uint32_t)(S * 4));
-      const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.delta + bh * S, (uint32_t)(S * 4));
+      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + bh * a.S + dc.off, (uint32_t)(S * 4));
+      const __amdgpu_buffer_rsrc_t rd =
+          make_rsrc(a.delta + bh * a.S + dc.off, (uint32_t)(S * 4));
 #pragma unroll
       for (int c = 0; c < (kBQ + 63) / 64; ++c) {
         if (kBQ >= 64 || lane < kBQ) {
@@ -1033,7 +1056,7 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
   }
 
   if (GLOB) {
-    float* part = a.gpart + ((int64_t)chunk * nbh + bhk) * a.G * 2 * D;
+    float* part = a.gpart + (((int64_t)chunk * nbh + bhk) * a.G + dc.gofs) * 2 * D;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const int row = kw + 16 * kb + l16;
@@ -1047,9 +1070,9 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
     }
     return;
   }
-  T* dkp = static_cast<T*>(a.dk) + b * a.dksb + hk * a.dksh;
-  T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh;
-  const float rsc = (a.relay && a.rscale) ? a.rscale[hk] : 1.f;
+  T* dkp = static_cast<T*>(a.dk) + b * a.dksb + hk * a.dksh + (int64_t)dc.off * a.dkss;
+  T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh + (int64_t)dc.off * a.dvss;
+  const float rsc = (relay && a.rscale) ? a.rscale[hk] : 1.f;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int j = kw + 16 * kb + l16;
@@ -1061,21 +1084,22 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a, int ntiles) {
     float gsc[5];
     int nm = 0;
     if (j == rblk * W) {
-      grow[nm] = rblk * a.rpb;
+      grow[nm] = rblk * rpb;
       gsc[nm++] = 1.f;
     }
-    if (a.relay) {
-      const int32_t* src = a.src + ((int64_t)bhk * (a.G / a.rpb) + rblk) * a.top_k;
+    if (relay) {
+      const int32_t* src = a.src + ((int64_t)bhk * a.NB + dc.bofs + rblk) * a.top_k;
       for (int t = 0; t < a.top_k; ++t) {
         if (src[t] == j) {
-          grow[nm] = rblk * a.rpb + 1 + t;
+          grow[nm] = rblk * rpb + 1 + t;
           gsc[nm++] = rsc;
         }
       }
     }
     for (int m = 0; m < nm; ++m) {
       for (int c = 0; c < a.nchunk; ++c) {
-        const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + grow[m]) * 2 * D;
+        const float* pk =
+            a.gpart + (((int64_t)c * nbh + bhk) * a.G + dc.gofs + grow[m]) * 2 * D;
 #pragma unroll
         for (int db = 0; db < D / 16; ++db) {
           dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
@@ -1106,30 +1130,35 @@ template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   using Tr = BwdTraits<T, D>;
   constexpr int kRows = 256 / (D / 8);
-  hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq), dim3(256),
-                     0, st, a);
-  const int qtiles = (a.S + Tr::kBM - 1) / Tr::kBM;
-  const int gtiles = (int)((a.G + Tr::kBK - 1) / Tr::kBK);
-  const int ktiles = (a.S + Tr::kBK - 1) / Tr::kBK;
+  if (a.group == 0)
+    hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq),
+                       dim3(256), 0, st, a);
+  // work items per document: query tiles (dQ), global-row tiles x query
+  // chunks (global dK/dV), key tiles (local dK/dV); all tiles are 128 rows
+  BwdArgs aq = a, ag = a, al = a;
+  set_items(aq.docs, [&](int d) { return (a.docs.len[d] + Tr::kBM - 1) / Tr::kBM; });
+  set_items(ag.docs, [&](int d) {
+    const int g = (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d] * a.docs.rpb[d];
+    return (g + Tr::kBK - 1) / Tr::kBK * a.nchunk;
+  });
+  set_items(al.docs, [&](int d) { return (a.docs.len[d] + Tr::kBK - 1) / Tr::kBK; });
+  const int nq = aq.docs.item0[a.docs.n], ng = ag.docs.item0[a.docs.n];
+  const int nl = al.docs.item0[a.docs.n];
   if constexpr (sizeof(T) == 2) {
-    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, 8 / kDqWaves>), dim3(qtiles * a.B * a.Hq),
-                       dim3(64 * kDqWaves), 0, st, a, qtiles);
+    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, 8 / kDqWaves>), dim3(nq * a.B * a.Hq),
+                       dim3(64 * kDqWaves), 0, st, aq);
     hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvWaves, 8 / kDkdvWaves, kDkdvGlobBQ>),
-                       dim3(gtiles * a.nchunk * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a,
-                       gtiles);
+                       dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, ag);
   } else {
-    hipLaunchKernelGGL((dq_kernel<T, D>), dim3(qtiles * a.B * a.Hq), dim3(256), 0, st, a, qtiles);
-    hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(gtiles * a.nchunk * a.B * a.Hkv),
-                       dim3(256), 0, st, a, gtiles);
+    hipLaunchKernelGGL((dq_kernel<T, D>), dim3(nq * a.B * a.Hq), dim3(256), 0, st, aq);
+    hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(ng * a.B * a.Hkv), dim3(256), 0, st, ag);
   }
-  if (a.dalpha && a.relay)
-    hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
+  if (a.dalpha) hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (sizeof(T) == 2)
     hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvWaves, 8 / kDkdvWaves, kDkdvLocalBQ>),
-                       dim3(ktiles * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, a, ktiles);
+                       dim3(nl * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, al);
   else
-    hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(ktiles * a.B * a.Hkv), dim3(256), 0, st,
-                       a, ktiles);
+    hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(nl * a.B * a.Hkv), dim3(256), 0, st, al);
   return hipGetLastError();
 }
 
@@ -1145,22 +1174,24 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
 
 }  // namespace
 
-size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int W, int64_t G, int* nchunk,
-                           int* chunk_len) {
-  (void)W;
-  // Enough global-row workgroups to cover the chip twice: tiles of 128 rows
-  // per (b, kv head), query range cut into chunks (multiples of 64 queries).
-  const int64_t gtiles = (G + 127) / 128;
+size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
+                           const int* W, const int* rpb, int64_t G, int* nchunk) {
+  // Enough global-row workgroups to cover the chip about twice: tiles of 128
+  // global rows per document and (b, kv head), each document's query range
+  // cut into the same number of chunks (multiples of 64 queries).
+  int64_t gtiles = 0;
+  int max_len = 1;
+  for (int d = 0; d < n; ++d) {
+    const int64_t g = (int64_t)(len[d] + W[d] - 1) / W[d] * rpb[d];
+    gtiles += (g + 127) / 128;
+    if (len[d] > max_len) max_len = len[d];
+  }
   const int64_t base = gtiles * B * Hkv;
   int64_t nc = (1024 + base - 1) / base;
-  const int64_t max_nc = (S + 255) / 256;
+  const int64_t max_nc = (max_len + 255) / 256;
   if (nc > max_nc) nc = max_nc;
   if (nc < 1) nc = 1;
-  int64_t len = (S + nc - 1) / nc;
-  len = (len + 63) / 64 * 64;
-  nc = (S + len - 1) / len;
   *nchunk = (int)nc;
-  *chunk_len = (int)len;
   const size_t delta = (((size_t)B * Hq * S * 4) + 255) / 256 * 256;
   const size_t part = (size_t)nc * B * Hkv * G * 2 * D * 4;
   return delta + part;

@@ -128,17 +128,19 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hq;
   const int bh = blockIdx.x % nbh;
-  const int tile = a.ntiles - 1 - (int)(blockIdx.x / nbh);
+  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  const int tile = (dc.len + Tr::kBM - 1) / Tr::kBM - 1 - dc.item;  // heaviest first
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int m0 = tile * Tr::kBM;
   const int q0 = m0 + wave * Tr::kQW;
-  const int S = a.S, W = a.W;
+  const int S = dc.len, W = dc.W, rpb = dc.rpb;
 
-  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
-  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
-  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh + (int64_t)dc.off * a.qss;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
+  float* lse = a.lse + (int64_t)bh * a.S + dc.off;
+  const int64_t gbase = ((int64_t)(b * a.Hkv + hk) * a.G + dc.gofs) * D;
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
 
@@ -196,10 +198,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   }
 
   // ---- phase 2+3: prefix of the packed strided/relay rows ---------------
-  const int gmax = glob_prefix(hi - 1, W, a.rpb);
-  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
-  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
-  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+  const int gmax = glob_prefix(hi - 1, W, rpb);
+  const int wg_lo = active ? glob_prefix(q0, W, rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, rpb), glob_prefix(qi[1], W, rpb)};
   const int g_end = (a.phases & 2) ? gmax : 0;
   for (int ts = 0; ts < g_end; ts += Tr::kBN) {
     stk.load(gkp, D, ts, 0, gmax, tid);
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   }
 
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) ln 2 ---------------------
-  T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
+  T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float l = group_sum(l_run[qb]);
@@ -237,7 +239,7 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
       }
     }
     if (g == 0)
-      a.lse[(int64_t)bh * S + qi[qb]] = (m_run[qb] + __builtin_amdgcn_logf(fmaxf(l, 1e-6f))) * kLn2;
+      lse[qi[qb]] = (m_run[qb] + __builtin_amdgcn_logf(fmaxf(l, 1e-6f))) * kLn2;
   }
 }
 
@@ -393,23 +395,25 @@ void fwd2_kernel(FwdArgs a) {
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hq;
   const int bh = blockIdx.x % nbh;
-  const int tile = a.ntiles - 1 - (int)(blockIdx.x / nbh);
+  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  const int tile = (dc.len + kBM - 1) / kBM - 1 - dc.item;  // heaviest first
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int m0 = tile * kBM;
   const int q0 = m0 + wave * kQW;
-  const int S = a.S, W = a.W;
+  const int S = dc.len, W = dc.W, rpb = dc.rpb;
 
-  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh;
-  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh;
-  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh;
-  const int64_t gbase = (int64_t)(b * a.Hkv + hk) * a.G * D;
+  const T* qp = static_cast<const T*>(a.q) + b * a.qsb + h * a.qsh + (int64_t)dc.off * a.qss;
+  const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
+  const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
+  float* lse = a.lse + (int64_t)bh * a.S + dc.off;
+  const int64_t gbase = ((int64_t)(b * a.Hkv + hk) * a.G + dc.gofs) * D;
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
 
   const int lo_k = max(0, m0 - W + 1);
   const int hi = min(S, m0 + kBM);
-  const int gmax = glob_prefix(hi - 1, W, a.rpb);
+  const int gmax = glob_prefix(hi - 1, W, rpb);
   const int nloc = (PH & 1) ? (hi - lo_k + kBN - 1) / kBN : 0;
   const int ntot = nloc + ((PH & 2) ? (gmax + kBN - 1) / kBN : 0);
 
@@ -467,9 +471,9 @@ void fwd2_kernel(FwdArgs a) {
   const bool active = q0 < S;
   const int q_last = min(q0 + kQW, S) - 1;
   const int w_lo = max(0, q0 - W + 1);
-  const int wg_lo = active ? glob_prefix(q0, W, a.rpb) : 0;
-  const int wg_hi = active ? glob_prefix(q_last, W, a.rpb) : 0;
-  const int glen[2] = {glob_prefix(qi[0], W, a.rpb), glob_prefix(qi[1], W, a.rpb)};
+  const int wg_lo = active ? glob_prefix(q0, W, rpb) : 0;
+  const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
+  const int glen[2] = {glob_prefix(qi[0], W, rpb), glob_prefix(qi[1], W, rpb)};
 
   // Local and global tiles share one body (parameters chosen per tile); the
   // loop is unrolled over the two stages.
@@ -504,7 +508,7 @@ void fwd2_kernel(FwdArgs a) {
     if (it + 1 < ntot) step(std::integral_constant<int, 1>{}, it + 1);
   }
 
-  T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh;
+  T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float l = group_sum(l_run[qb]);
@@ -519,7 +523,7 @@ void fwd2_kernel(FwdArgs a) {
       *reinterpret_cast<uint2*>(orow + 16 * db + 4 * g) = *reinterpret_cast<const uint2*>(e);
     }
     if (g == 0)
-      a.lse[(int64_t)bh * S + qi[qb]] = (m_run[qb] + __builtin_amdgcn_logf(fmaxf(l, 1e-6f))) * kLn2;
+      lse[qi[qb]] = (m_run[qb] + __builtin_amdgcn_logf(fmaxf(l, 1e-6f))) * kLn2;
   }
 }
 
@@ -532,8 +536,9 @@ template <typename T>
 hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     FwdArgs b = a;
-    b.ntiles = (a.S + 32 * kFwdWaves - 1) / (32 * kFwdWaves);
-    const dim3 grid(b.ntiles * b.B * b.Hq), block(64 * kFwdWaves);
+    constexpr int kBM = 32 * kFwdWaves;
+    set_items(b.docs, [&](int d) { return (b.docs.len[d] + kBM - 1) / kBM; });
+    const dim3 grid(b.docs.item0[b.docs.n] * b.B * b.Hq), block(64 * kFwdWaves);
     auto go = [&](auto dc) {
       constexpr int Dc = decltype(dc)::value;
       switch (a.phases) {
@@ -549,11 +554,13 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
       default: return hipErrorInvalidValue;
     }
   } else {
-    const dim3 grid(a.ntiles * a.B * a.Hq);
+    FwdArgs b = a;
+    set_items(b.docs, [&](int d) { return (b.docs.len[d] + 127) / 128; });
+    const dim3 grid(b.docs.item0[b.docs.n] * b.B * b.Hq);
     switch (D) {
-      case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
-      case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
-      case 128: hipLaunchKernelGGL((fwd_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+      case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, b); break;
+      case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, b); break;
+      case 128: hipLaunchKernelGGL((fwd_kernel<T, 128>), grid, dim3(256), 0, st, b); break;
       default: return hipErrorInvalidValue;
     }
   }

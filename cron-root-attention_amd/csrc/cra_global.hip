@@ -28,22 +28,25 @@ __global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
   constexpr int kLPR = D / 8;        // lanes per row
   constexpr int kNRG = 256 / kLPR;   // row groups per workgroup
   constexpr int kW16 = Frag<T>::kWords;
-  const int r = blockIdx.x;
+  const Doc dc = find_doc(a.docs, blockIdx.x);
+  const int r = dc.item;  // block of the document
+  const int W = dc.W, rpb = dc.rpb;
+  const bool relay = rpb > 1;
   const int bh = blockIdx.y;
   const int b = bh / a.Hkv, h = bh % a.Hkv;
-  const T* kb = static_cast<const T*>(a.k) + b * a.ksb + h * a.ksh;
-  const T* vb = static_cast<const T*>(a.v) + b * a.vsb + h * a.vsh;
+  const T* kb = static_cast<const T*>(a.k) + b * a.ksb + h * a.ksh + (int64_t)dc.off * a.kss;
+  const T* vb = static_cast<const T*>(a.v) + b * a.vsb + h * a.vsh + (int64_t)dc.off * a.vss;
   const int tid = threadIdx.x;
-  const int row0 = r * a.W;
+  const int row0 = r * W;  // rows of the document
 
   __shared__ float s_norm[kNRG * 4];
   __shared__ int s_idx[kNRG * 4];
   __shared__ int s_sel[4];
 
-  if (a.relay) {
+  if (relay) {
     const int li = tid % kLPR;
     const int rg = tid / kLPR;
-    const int nrows = min(a.W, a.S - row0);
+    const int nrows = min(W, dc.len - row0);
     float bn[4] = {kSentinel, kSentinel, kSentinel, kSentinel};
     int bi[4] = {0, 0, 0, 0};
     for (int base = 0; base < nrows; base += kNRG) {  // uniform trip count
@@ -102,18 +105,18 @@ __global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
         s_sel[j] = row0 + s_idx[best];
         s_norm[best] = -__builtin_huge_valf();
       }
-      int32_t* src = a.src + (int64_t)bh * a.NB * a.top_k + (int64_t)r * a.top_k;
+      int32_t* src = a.src + ((int64_t)bh * a.NB + dc.bofs + r) * a.top_k;
       for (int j = 0; j < a.top_k; ++j) src[j] = s_sel[j];
     }
     __syncthreads();
   }
 
   // Emit rows: slot 0 = strided row r*W, slots 1..top_k = relay rows.
-  T* gk = static_cast<T*>(a.gk) + ((int64_t)bh * a.G + (int64_t)r * a.rpb) * D;
-  T* gv = static_cast<T*>(a.gv) + ((int64_t)bh * a.G + (int64_t)r * a.rpb) * D;
+  T* gk = static_cast<T*>(a.gk) + ((int64_t)bh * a.G + dc.gofs + (int64_t)r * rpb) * D;
+  T* gv = static_cast<T*>(a.gv) + ((int64_t)bh * a.G + dc.gofs + (int64_t)r * rpb) * D;
   const int cg = tid % (D / 8);
-  const float sc = (a.relay && a.scale) ? a.scale[h] : 1.f;
-  for (int slot = tid / (D / 8); slot < a.rpb; slot += 256 / (D / 8)) {
+  const float sc = (relay && a.scale) ? a.scale[h] : 1.f;
+  for (int slot = tid / (D / 8); slot < rpb; slot += 256 / (D / 8)) {
     const int row = slot == 0 ? row0 : s_sel[slot - 1];
     const uint4* pk = reinterpret_cast<const uint4*>(kb + (int64_t)row * a.kss + cg * 8);
     const uint4* pv = reinterpret_cast<const uint4*>(vb + (int64_t)row * a.vss + cg * 8);
@@ -143,8 +146,10 @@ __global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
 }
 
 template <typename T>
-hipError_t launch_T(int D, const GlobalArgs& a, int B, hipStream_t st) {
-  dim3 grid(a.NB, B * a.Hkv);
+hipError_t launch_T(int D, const GlobalArgs& args, int B, hipStream_t st) {
+  GlobalArgs a = args;  // work items: the W-blocks of each document
+  set_items(a.docs, [&](int d) { return (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d]; });
+  dim3 grid(a.docs.item0[a.docs.n], B * a.Hkv);
   switch (D) {
     case 32: hipLaunchKernelGGL((build_global_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
     case 64: hipLaunchKernelGGL((build_global_kernel<T, 64>), grid, dim3(256), 0, st, a); break;

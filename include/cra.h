@@ -134,6 +134,51 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
             const int32_t* relay_src, const float* relay_scale, cra_tensor dq, cra_tensor dk,
             cra_tensor dv, float* dalpha, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Documents packed along S (varlen): document d is rows
+ * cu_seqlens[d] .. cu_seqlens[d+1]-1 of every [B, H, S, D] tensor and is
+ * attended on its own (nothing across documents), with its own window and
+ * relay switch. All three arrays are host memory, read during the call only.
+ * In the cra_problem of a *_varlen call S is the packed length
+ * cu_seqlens[n_docs]; W and relay are not used; top_k applies to every
+ * document with relay on. */
+typedef struct {
+  int32_t n_docs;
+  const int32_t* cu_seqlens; /* n_docs + 1 entries rising strictly from 0 to S */
+  const int32_t* window;     /* n_docs entries, 1 <= window[d] <= length of d
+                                (the reference: ceil(sqrt(length)), core.py:3479) */
+  const int32_t* relay;      /* n_docs entries, 0 or 1 (the reference: length > 2048,
+                                core.py:3507) */
+} cra_docs;
+
+/* Sizes of the packed global rows and relay source rows of a varlen call,
+ * per (b, kv head): the documents' blocks in document order, document d
+ * taking ceil(len/W) * (1 + top_k) (relay) or ceil(len/W) rows of glob_k/v
+ * laid out as for one sequence (cra_global_rows), and ceil(len/W) * top_k
+ * relay_src entries (row indices relative to the document's first row; the
+ * entries of a document without relay are not written). */
+int cra_varlen_sizes(const cra_problem* p, const cra_docs* docs, int64_t* global_rows,
+                     int64_t* relay_src_len);
+
+/* The varlen forms of cra_build_global, cra_fwd, cra_bwd_workspace_bytes and
+ * cra_bwd: same buffers and contracts with the sizes of cra_varlen_sizes; one
+ * call covers every document (launches take up to 64 documents each).
+ * relay_scale and dalpha are per kv head over all documents.
+ * Replace the per-document loop of `cron_root_attention_varlen` (reference
+ * core.py:3836-3954), which calls the whole op once per document on narrow()
+ * views and copies each result into the output. */
+int cra_build_global_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor k,
+                            cra_tensor v, void* glob_k, void* glob_v, int32_t* relay_src,
+                            const float* relay_scale, void* stream);
+int cra_fwd_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor q, cra_tensor k,
+                   cra_tensor v, const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                   void* stream);
+size_t cra_bwd_workspace_bytes_varlen(const cra_problem* p, const cra_docs* docs);
+int cra_bwd_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor q, cra_tensor k,
+                   cra_tensor v, cra_tensor o, cra_tensor dout, const float* lse,
+                   const void* glob_k, const void* glob_v, const int32_t* relay_src,
+                   const float* relay_scale, cra_tensor dq, cra_tensor dk, cra_tensor dv,
+                   float* dalpha, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Device facts for get_num_sms()/get_gpu_info() (reference core.py:137-188,
  * __init__.py:183-202). */
 int cra_device_info(int32_t device, cra_device_info_t* out);

@@ -354,6 +354,55 @@ def forward_backward(q, k, v, dO, plan: Plan, kv_groups: int = 1,
     return o.detach(), lse.detach(), src, grads
 
 
+# ---------------------------------------------------------------------------
+# Packed documents (varlen, core.py:3836-3954)
+# ---------------------------------------------------------------------------
+
+def varlen_plans(cu_seqlens, mode: str = "kernel", top_k: int = 2) -> list:
+    """One plan per document, from the document's own length: the reference
+    calls the whole op once per document on a narrow() view
+    (core.py:3911-3952), so W and the relay switch follow each length."""
+    return [make_plan(e - s, mode, top_k) for s, e in zip(cu_seqlens, cu_seqlens[1:])]
+
+
+def forward_varlen(q, k, v, cu_seqlens, plans=None, kv_groups: int = 1,
+                   relay_scale: Optional[torch.Tensor] = None, top_k: int = 2, **kw):
+    """Documents [cu_seqlens[d], cu_seqlens[d+1]) attended on their own and the
+    results concatenated along S (core.py:3923-3954: one call per document,
+    each written into its slice of the output); differentiable.
+    Returns (o, lse, [src of each document])."""
+    plans = varlen_plans(cu_seqlens, top_k=top_k) if plans is None else plans
+    outs, lses, srcs = [], [], []
+    for (s, e), pl in zip(zip(cu_seqlens, cu_seqlens[1:]), plans):
+        o, lse, src = forward(q[:, :, s:e], k[:, :, s:e], v[:, :, s:e], pl, kv_groups,
+                              relay_scale=relay_scale if pl.relay else None, **kw)
+        outs.append(o)
+        lses.append(lse)
+        srcs.append(src)
+    return torch.cat(outs, dim=2), torch.cat(lses, dim=2), srcs
+
+
+def forward_backward_varlen(q, k, v, dO, cu_seqlens, plans=None, kv_groups: int = 1,
+                            relay_log_scale: Optional[torch.Tensor] = None, top_k: int = 2):
+    """Gradients of :func:`forward_varlen` by fp64 autograd; d(relay_log_scale)
+    sums over every document with relay, the parameter being shared by the
+    per-document calls (core.py:3911-3952 pass the same tensor)."""
+    q64 = q.detach().to(torch.float64).requires_grad_(True)
+    k64 = k.detach().to(torch.float64).requires_grad_(True)
+    v64 = v.detach().to(torch.float64).requires_grad_(True)
+    a64 = scale = None
+    if relay_log_scale is not None:
+        a64 = relay_log_scale.detach().to(torch.float64).requires_grad_(True)
+        scale = torch.exp(a64)
+    o, lse, srcs = forward_varlen(q64, k64, v64, cu_seqlens, plans, kv_groups, relay_scale=scale,
+                                  top_k=top_k)
+    o.backward(dO.to(torch.float64))
+    grads = dict(dq=q64.grad, dk=k64.grad, dv=v64.grad)
+    if a64 is not None:
+        grads["dalpha"] = a64.grad if a64.grad is not None else torch.zeros_like(a64)
+    return o.detach(), lse.detach(), srcs, grads
+
+
 def causal_sdpa_reference(q, k, v):
     """Dense causal attention in fp64 (the library routine the first W rows
     of every sequence must reduce to: their sets are pure causal prefixes)."""

@@ -137,3 +137,84 @@ def test_build_global_requires_src_with_relay():
     t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
     rc = lib.cra_build_global(ctypes.byref(prob()), t, t, 0x10000, 0x10000, None, None, None)
     assert rc == N.E_INVALID and "relay_src" in lib.cra_last_error().decode()
+
+
+# ------------------------------------------------------------------ varlen
+
+def vprob(S, **kw):
+    base = dict(B=2, H_q=4, H_kv=2, S=S, D=64, W=0, relay=0, top_k=2, dtype=0, scale=0.125)
+    base.update(kw)
+    return N.CraProblem(**base)
+
+
+def sizes(p, docs):
+    lib = N.load_library()
+    g, r = ctypes.c_int64(-1), ctypes.c_int64(-1)
+    rc = lib.cra_varlen_sizes(ctypes.byref(p), ctypes.byref(docs.struct), ctypes.byref(g),
+                              ctypes.byref(r))
+    return rc, g.value, r.value
+
+
+def test_varlen_sizes():
+    docs = N.Docs([0, 100, 2149, 5149], [10, 46, 55], [0, 1, 1])
+    rc, g, r = sizes(vprob(5149), docs)
+    assert rc == N.OK
+    assert g == 10 + 45 * 3 + 55 * 3          # blocks x (1 + top_k) for relay documents
+    assert r == (10 + 45 + 55) * 2            # relay_src entries span every document's blocks
+    rc, g, r = sizes(vprob(5149, top_k=9), N.Docs([0, 100, 2149, 5149], [10, 46, 55], [0, 0, 0]))
+    assert rc == N.OK and g == 110 and r == 0  # top_k is only checked when a document relays
+
+
+def test_varlen_one_document_matches_plain_sizes():
+    lib = N.load_library()
+    p = prob()
+    docs = N.Docs([0, p.S], [p.W], [p.relay])
+    rc, g, _ = sizes(p, docs)
+    assert rc == N.OK and g == lib.cra_global_rows(ctypes.byref(p))
+    assert (lib.cra_bwd_workspace_bytes_varlen(ctypes.byref(p), ctypes.byref(docs.struct))
+            == lib.cra_bwd_workspace_bytes(ctypes.byref(p)))
+
+
+@pytest.mark.parametrize("cu,W,R,kw,msg", [
+    ([1, 50, 100], [5, 5], [0, 0], {}, "from 0"),
+    ([0, 50, 99], [5, 5], [0, 0], {}, "from 0"),
+    ([0, 60, 60, 100], [5, 5, 5], [0, 0, 0], {}, "rise strictly"),
+    ([0, 50, 100], [0, 5], [0, 0], {}, "window"),
+    ([0, 50, 100], [5, 51], [0, 0], {}, "window"),
+    ([0, 50, 100], [5, 5], [0, 2], {}, "relay"),
+    ([0, 50, 100], [5, 5], [0, 1], dict(top_k=5), "top_k"),
+])
+def test_varlen_rejects_bad_documents(cu, W, R, kw, msg):
+    lib = N.load_library()
+    rc, _, _ = sizes(vprob(100, **kw), N.Docs(cu, W, R))
+    assert rc == N.E_INVALID
+    assert msg in lib.cra_last_error().decode()
+
+
+def test_varlen_rejects_missing_arrays():
+    lib = N.load_library()
+    p = vprob(100)
+    bad = N.CraDocs(2, None, None, None)
+    assert lib.cra_varlen_sizes(ctypes.byref(p), ctypes.byref(bad), None, None) == N.E_INVALID
+    assert lib.cra_varlen_sizes(ctypes.byref(p), None, None, None) == N.E_INVALID
+    zero = N.Docs([0], [], [])
+    assert lib.cra_varlen_sizes(ctypes.byref(p), ctypes.byref(zero.struct), None, None) == N.E_INVALID
+    assert lib.cra_bwd_workspace_bytes_varlen(ctypes.byref(p), ctypes.byref(bad)) == 0
+
+
+def test_varlen_entry_points_validate_before_launch():
+    lib = N.load_library()
+    t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 64)
+    p = vprob(100)
+    docs = N.Docs([0, 30, 100], [6, 9], [0, 1])
+    d = ctypes.byref(docs.struct)
+    rc = lib.cra_build_global_varlen(ctypes.byref(p), d, t, t, 0x10000, 0x10000, None, None, None)
+    assert rc == N.E_INVALID and "relay_src" in lib.cra_last_error().decode()
+    odd = N.CraTensor(0x10002, 1 << 20, 1 << 16, 64)
+    rc = lib.cra_fwd_varlen(ctypes.byref(p), d, odd, t, t, 0x10000, 0x10000, t, 0x10000, None)
+    assert rc == N.E_LAYOUT
+    need = lib.cra_bwd_workspace_bytes_varlen(ctypes.byref(p), d)
+    assert need > 0
+    rc = lib.cra_bwd_varlen(ctypes.byref(p), d, t, t, t, t, t, 0x10000, 0x10000, 0x10000,
+                            0x10000, None, t, t, t, None, 0x10000, need - 1, None)
+    assert rc == N.E_WORKSPACE

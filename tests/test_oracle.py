@@ -327,3 +327,81 @@ def test_cpu_port_matches_oracle_and_golden():
     assert np.abs(o[:, :, z["rows"]].numpy() - z["o_rows"]).max() < 5e-6
     part = cpu_port.cra_cpu_chunked(q, k, v, plan, q_rows=(1000, 1300))
     assert torch.allclose(part, o[:, :, 1000:1300], atol=1e-6)
+
+
+# ------------------------------------------------------------- varlen (packed)
+
+def test_varlen_single_document_is_forward():
+    torch.manual_seed(11)
+    S, D = 300, 8
+    q, k, v = (torch.randn(1, 2, S, D, dtype=torch.float64) for _ in range(3))
+    o1, l1, _ = O.forward_varlen(q, k, v, [0, S])
+    o2, l2, _ = O.forward(q, k, v, O.make_plan(S))
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_varlen_plans_follow_each_length():
+    plans = O.varlen_plans([0, 100, 2149, 5149])
+    assert [(p.S, p.W, p.relay) for p in plans] == [(100, 10, False), (2049, 46, True),
+                                                     (3000, 55, True)]
+
+
+def test_varlen_bruteforce_packed_masks():
+    """Every packed query against an explicit softmax over the keys of its own
+    document only (offsets, per-document plans, no cross-document keys)."""
+    torch.manual_seed(12)
+    cu = [0, 1, 41, 101, 130]
+    plans = [O.make_plan(1), O.make_plan(40), O.Plan(60, 8, True, 2), O.Plan(29, 5, True, 1)]
+    S, D = cu[-1], 4
+    q, k, v = (torch.randn(1, 1, S, D, dtype=torch.float64) for _ in range(3))
+    o, lse, srcs = O.forward_varlen(q, k, v, cu, plans)
+    scale = 1 / math.sqrt(D)
+    for d, (s, e) in enumerate(zip(cu, cu[1:])):
+        pl = plans[d]
+        srcl = (srcs[d][0, 0].view(-1, pl.top_k).tolist() if pl.relay else None)
+        for i in range(s, e):
+            rows = [s + j for j in O.attend_set_bruteforce(i - s, pl, srcl)]
+            assert all(s <= j <= i for j in rows)
+            sc = [float((q[0, 0, i] * k[0, 0, j]).sum()) * scale for j in rows]
+            m = max(sc)
+            w = [math.exp(x - m) for x in sc]
+            z = sum(w)
+            ref = sum(wi * v[0, 0, j] for wi, j in zip(w, rows)) / z
+            assert torch.allclose(o[0, 0, i], ref, atol=1e-12), (d, i)
+            assert abs(float(lse[0, 0, i]) - (m + math.log(z))) < 1e-12
+
+
+def test_varlen_documents_are_isolated():
+    torch.manual_seed(13)
+    cu = [0, 90, 200]
+    q, k, v = (torch.randn(1, 2, 200, 8, dtype=torch.float64) for _ in range(3))
+    o, _, _ = O.forward_varlen(q, k, v, cu)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, :90] += 3.0
+    v2[:, :, :90] -= 1.0
+    o2, _, _ = O.forward_varlen(q, k2, v2, cu)
+    assert torch.equal(o[:, :, 90:], o2[:, :, 90:])
+    assert not torch.allclose(o[:, :, :90], o2[:, :, :90])
+
+
+def test_varlen_relay_scale_gradient_sums_documents():
+    """d(alpha) of the packed call by central difference, relay in two documents."""
+    torch.manual_seed(14)
+    cu = [0, 50, 120]
+    plans = [O.Plan(50, 7, True, 2), O.Plan(70, 9, True, 2)]
+    q, k, v, dO = (torch.randn(1, 2, 120, 8) for _ in range(4))
+    alpha = torch.tensor([0.25, -0.4], dtype=torch.float64)
+    _, _, srcs, g = O.forward_backward_varlen(q, k, v, dO, cu, plans, relay_log_scale=alpha)
+    eps = 1e-6
+
+    def L(a):
+        parts = [O.forward(q[:, :, s:e], k[:, :, s:e], v[:, :, s:e], pl, src=src,
+                           relay_scale=torch.exp(a))[0]
+                 for (s, e), pl, src in zip(zip(cu, cu[1:]), plans, srcs)]
+        return float((torch.cat(parts, 2) * dO.double()).sum())
+
+    for h in range(2):
+        e = torch.zeros(2, dtype=torch.float64)
+        e[h] = eps
+        fd = (L(alpha + e) - L(alpha - e)) / (2 * eps)
+        assert abs(fd - float(g["dalpha"][h])) < 1e-6
