@@ -888,7 +888,6 @@ template <typename T, int D, bool GLOB, int NW, int KB, int BQ>
 __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
   using Tile = SwzTile<D, BQ>;
   constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = BQ;
-  static_assert(kBK == 128, "128 key rows per workgroup");
   static_assert(BQ == 32 || BQ == 64 || BQ == 128, "query tile rows");
   // Two pipeline stages as separate LDS objects (see fwd2_kernel): Q and dO
   // rows, and their LSE and Delta.
@@ -1115,14 +1114,19 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
   }
 }
 
-// dK/dV workgroups: 8 waves of 16 key rows (two waves per SIMD, no register
-// file spill into AGPR copies at D = 128). dQ workgroups: 4 waves of 32
-// queries (each K/V fragment read from LDS serves two query blocks; 8 waves
-// of 16 queries measured 27% slower at D = 128).
-constexpr int kDkdvWaves = 8;
+// dK/dV workgroups: waves of 16 key rows (no register file spill into AGPR
+// copies at D = 128; 32 rows per wave measured 14% slower). The global-row
+// kernel uses 8 waves (128 rows; 4 waves measured 3% slower); the local
+// kernel 4 waves (64 rows: its band of queries, 64 + W - 1, wastes fewer
+// pairs than with 128 rows; measured 7% faster). dQ workgroups: 4 waves of
+// 32 queries (each K/V fragment read from LDS serves two query blocks; 8
+// waves of 16 queries measured 27% slower at D = 128).
+constexpr int kDkdvGlobWaves = 8;
+constexpr int kDkdvLocalWaves = 4;
+constexpr int kDkdvKB = 1;  // 16-key blocks per wave
 constexpr int kDqWaves = 4;
-// Query rows per dK/dV tile (32 and 128 measured 6% and 3% slower on the
-// local kernel, equal on the global one).
+// Query rows per dK/dV tile (with 8-wave local workgroups 32 and 128
+// measured 6% and 3% slower, equal on the global kernel).
 constexpr int kDkdvGlobBQ = 64;
 constexpr int kDkdvLocalBQ = 64;
 
@@ -1137,26 +1141,29 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   // chunks (global dK/dV), key tiles (local dK/dV); all tiles are 128 rows
   BwdArgs aq = a, ag = a, al = a;
   set_items(aq.docs, [&](int d) { return (a.docs.len[d] + Tr::kBM - 1) / Tr::kBM; });
+  constexpr bool kMfma = sizeof(T) == 2;
+  constexpr int kGK = kMfma ? 16 * kDkdvGlobWaves * kDkdvKB : Tr::kBK;   // rows per workgroup
+  constexpr int kLK = kMfma ? 16 * kDkdvLocalWaves * kDkdvKB : Tr::kBK;
   set_items(ag.docs, [&](int d) {
     const int g = (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d] * a.docs.rpb[d];
-    return (g + Tr::kBK - 1) / Tr::kBK * a.nchunk;
+    return (g + kGK - 1) / kGK * a.nchunk;
   });
-  set_items(al.docs, [&](int d) { return (a.docs.len[d] + Tr::kBK - 1) / Tr::kBK; });
+  set_items(al.docs, [&](int d) { return (a.docs.len[d] + kLK - 1) / kLK; });
   const int nq = aq.docs.item0[a.docs.n], ng = ag.docs.item0[a.docs.n];
   const int nl = al.docs.item0[a.docs.n];
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, 8 / kDqWaves>), dim3(nq * a.B * a.Hq),
                        dim3(64 * kDqWaves), 0, st, aq);
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvWaves, 8 / kDkdvWaves, kDkdvGlobBQ>),
-                       dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, ag);
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvGlobWaves, kDkdvKB, kDkdvGlobBQ>),
+                       dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvGlobWaves), 0, st, ag);
   } else {
     hipLaunchKernelGGL((dq_kernel<T, D>), dim3(nq * a.B * a.Hq), dim3(256), 0, st, aq);
     hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(ng * a.B * a.Hkv), dim3(256), 0, st, ag);
   }
   if (a.dalpha) hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvWaves, 8 / kDkdvWaves, kDkdvLocalBQ>),
-                       dim3(nl * a.B * a.Hkv), dim3(64 * kDkdvWaves), 0, st, al);
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvLocalWaves, kDkdvKB, kDkdvLocalBQ>),
+                       dim3(nl * a.B * a.Hkv), dim3(64 * kDkdvLocalWaves), 0, st, al);
   else
     hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(nl * a.B * a.Hkv), dim3(256), 0, st, al);
   return hipGetLastError();
