@@ -9,7 +9,8 @@
 // dQ_i += scale dS k_j, dK_j += scale dS q_i, dV_j += P dO_i.
 //
 // This build keeps every accumulation in fp32 and rounds once:
-//   1. delta_kernel      Delta = rowsum(O * dO)                       (fp32)
+//   1. delta_kernel      Delta = rowsum(O * dO)  (fp32 inputs; for fp16/bf16
+//                        dq2_kernel computes Delta of its queries and stores it)
 //   2. dq_kernel         query-centric: local band + global prefix -> dQ
 //   3. dkdv_kernel<GLOB> packed global rows (strided + relay), query range
 //                        split in chunks -> fp32 partials in the workspace
@@ -700,7 +701,7 @@ void dq2_kernel(BwdArgs a) {
   const T* kp = static_cast<const T*>(a.k) + b * a.ksb + hk * a.ksh + (int64_t)dc.off * a.kss;
   const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
   const float* lse = a.lse + (int64_t)bh * a.S + dc.off;
-  const float* delta = a.delta + (int64_t)bh * a.S + dc.off;
+  float* delta = a.delta + (int64_t)bh * a.S + dc.off;
   const int64_t gbase = ((int64_t)(b * a.Hkv + hk) * a.G + dc.gofs) * D;
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
@@ -738,22 +739,35 @@ void dq2_kernel(BwdArgs a) {
   Frag<T> qf[QB][D / 32], df[QB][D / 32];
   int qi[QB];
   float lse2[QB], dl[QB];
+  // Delta = rowsum(O * dO) of this wave's queries, computed here and stored
+  // for the dK/dV kernels: lane (l16, g) sums its 32 columns, then the four
+  // lanes of a query add theirs in a fixed order.
+  const T* opp = static_cast<const T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
     const bool ok = qi[qb] < S;
     lse2[qb] = ok ? lse[qi[qb]] * kLog2e : 0.f;
-    dl[qb] = ok ? delta[qi[qb]] : 0.f;
+    float od = 0.f;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) {
       if (ok) {
         qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qi[qb] * a.qss + 32 * c + 8 * g);
         df[qb][c] = lds_frag_row<T>(dop + (int64_t)qi[qb] * a.doss + 32 * c + 8 * g);
+        const Frag<T> of = lds_frag_row<T>(opp + (int64_t)qi[qb] * a.oss + 32 * c + 8 * g);
+        const T* eo = reinterpret_cast<const T*>(of.w);
+        const T* ed = reinterpret_cast<const T*>(df[qb][c].w);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) od = fmaf(to_f32(eo[i]), to_f32(ed[i]), od);
       } else {
         zero_frag(qf[qb][c]);
         zero_frag(df[qb][c]);
       }
     }
+    od += __shfl_xor(od, 16);
+    od += __shfl_xor(od, 32);
+    dl[qb] = od;
+    if (ok && g == 0) delta[qi[qb]] = od;
   }
   const float c2 = a.scale * kLog2e;
   f32x4 dqa[D / 16][QB];
@@ -1134,7 +1148,8 @@ template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   using Tr = BwdTraits<T, D>;
   constexpr int kRows = 256 / (D / 8);
-  if (a.group == 0)
+  // fp16/bf16: dq2_kernel computes Delta for its own queries and stores it
+  if (sizeof(T) == 4 && a.group == 0)
     hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq),
                        dim3(256), 0, st, a);
   // work items per document: query tiles (dQ), global-row tiles x query
