@@ -1002,41 +1002,55 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
   const int full_hi = GLOB ? q_hi : kw + W;  // exclusive
   const float c2 = a.scale * kLog2e;
 
-  // Tile `it` = query tile it % ntile_q of group head it / ntile_q; buffer
-  // resources are built per head (scalar work).
-  auto load_tile = [&](int it, char (&dst)[2][Tile::kBytes], float (&dsl)[2][kBQ]) {
-    const int j = it / ntile_q;
-    const int ts = q_lo + (it - j * ntile_q) * kBQ;
+  // Tiles run head by head of the kv group (tile `it` is query tile
+  // it % ntile_q of group head it / ntile_q). The (head, tile) counters of
+  // the next tile to load and of the tile being computed advance by one per
+  // step, and the buffer resources are rebuilt only when the head changes:
+  // no per-tile division or 64-bit address arithmetic.
+  struct HeadRes {
+    __amdgpu_buffer_rsrc_t q, o, l, d;
+  };
+  auto head_res = [&](int j) {
     const int hq = hk * grp + j;
     const int64_t bh = (int64_t)b * a.Hq + hq;
-    // rows at or past q_hi load as zeros
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
-        static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh + (int64_t)dc.off * a.qss,
-        (uint32_t)((q_hi - 1) * qbytes + D * 2));
-    const __amdgpu_buffer_rsrc_t ro = make_rsrc(
+    // query rows at or past q_hi load as zeros
+    HeadRes r;
+    r.q = make_rsrc(static_cast<const T*>(a.q) + b * a.qsb + hq * a.qsh + (int64_t)dc.off * a.qss,
+                    (uint32_t)((q_hi - 1) * qbytes + D * 2));
+    r.o = make_rsrc(
         static_cast<const T*>(a.dout) + b * a.dosb + hq * a.dosh + (int64_t)dc.off * a.doss,
         (uint32_t)((q_hi - 1) * obytes + D * 2));
-    Fill::load(dst[0], rq, fq, qbytes, ts, wave);
-    Fill::load(dst[1], ro, fo, obytes, ts, wave);
+    r.l = make_rsrc(a.lse + bh * a.S + dc.off, (uint32_t)(S * 4));
+    r.d = make_rsrc(a.delta + bh * a.S + dc.off, (uint32_t)(S * 4));
+    return r;
+  };
+  HeadRes ld_res = head_res(0);
+  int ld_j = 0, ld_t = 0;  // next tile to load
+  auto load_tile = [&](char (&dst)[2][Tile::kBytes], float (&dsl)[2][kBQ]) {
+    const int ts = q_lo + ld_t * kBQ;
+    Fill::load(dst[0], ld_res.q, fq, qbytes, ts, wave);
+    Fill::load(dst[1], ld_res.o, fo, obytes, ts, wave);
     // one lane per query row of the tile (lane i of pass c lands at
     // dsl[.][64 c + i])
     if (wave == 0) {
-      const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lse + bh * a.S + dc.off, (uint32_t)(S * 4));
-      const __amdgpu_buffer_rsrc_t rd =
-          make_rsrc(a.delta + bh * a.S + dc.off, (uint32_t)(S * 4));
 #pragma unroll
       for (int c = 0; c < (kBQ + 63) / 64; ++c) {
         if (kBQ >= 64 || lane < kBQ) {
           const int qrow = min(ts + 64 * c + lane, q_hi - 1);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, CRA_LDS(&dsl[0][64 * c]), 4, qrow * 4, 0,
-                                                   0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, CRA_LDS(&dsl[1][64 * c]), 4, qrow * 4, 0,
-                                                   0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ld_res.l, CRA_LDS(&dsl[0][64 * c]), 4,
+                                                   qrow * 4, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(ld_res.d, CRA_LDS(&dsl[1][64 * c]), 4,
+                                                   qrow * 4, 0, 0, 0);
         }
       }
     }
+    if (++ld_t == ntile_q) {
+      ld_t = 0;
+      if (++ld_j < grp) ld_res = head_res(ld_j);
+    }
   };
-  if (ntot > 0) load_tile(0, stage0, sld0);
+  if (ntot > 0) load_tile(stage0, sld0);
+  int cu_t = 0;  // query tile being computed
 
   auto step = [&](auto BUFC, int it) {
     constexpr int BUF = decltype(BUFC)::value;
@@ -1046,12 +1060,12 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
     __syncthreads();
     if (it + 1 < ntot) {
       if (BUF)
-        load_tile(it + 1, stage0, sld0);
+        load_tile(stage0, sld0);
       else
-        load_tile(it + 1, stage1, sld1);
+        load_tile(stage1, sld1);
     }
-    const int j = it / ntile_q;
-    const int ts = q_lo + (it - j * ntile_q) * kBQ;
+    const int ts = q_lo + cu_t * kBQ;
+    if (++cu_t == ntile_q) cu_t = 0;
     const int t_last = min(ts + kBQ, q_hi) - 1;
     if (active && t_last >= wq_lo && ts < wq_hi) {
       const bool full = ts >= full_lo && ts + kBQ <= full_hi && ts + kBQ <= q_hi;
