@@ -621,10 +621,12 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
                                          const Frag<T> (&df)[QB][D / 32],
                                          f32x4 (&dqa)[D / 16][QB], const float (&lse2)[QB],
                                          const float (&dl)[QB], float c2, int g,
-                                         const TileMask& mk) {
+                                         const TileMask& mk, bool half0, bool half1) {
   using Tile = SwzTile<D, 64>;
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
+    // masked tiles: a 32-key half with no key visible to the wave is skipped
+    if (MASK && !(kc ? half1 : half0)) continue;
     float ds[2][QB][4];  // [h][qb][r]
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -807,10 +809,14 @@ void dq2_kernel(BwdArgs a) {
       mk.span[qb] = loc ? (unsigned)(W - 1) : 0x7fffffffu;
     }
     if (work) {
+      // keys of the tile visible to some query of the wave: [vis_lo, vis_hi]
+      const int vis_lo = loc ? w_lo - ts : 0;
+      const int vis_hi = loc ? q_last - ts : wg_hi - 1 - ts;
+      const bool half0 = vis_lo <= 31, half1 = vis_hi >= 32;
       if (full)
-        dq2_tile<T, D, QB, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
+        dq2_tile<T, D, QB, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, true, true);
       else
-        dq2_tile<T, D, QB, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk);
+        dq2_tile<T, D, QB, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, half0, half1);
     }
   };
   for (int it = 0; it < ntot; it += 2) {

@@ -374,6 +374,36 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
   }
 }
 
+// One 32-key half kc of a masked tile, for tiles whose other half has no
+// key visible to any of the wave's queries (window and prefix edges).
+template <typename T, int D, int BN>
+__device__ __forceinline__ void attend_half(const char* tK, const char* tV, int kc,
+                                            const Fwd2Lane<D>& lo, const Frag<T> (&qf)[2][D / 32],
+                                            f32x4 (&acc)[D / 16][2], float (&m_run)[2],
+                                            float (&l_run)[2], float c2, int g,
+                                            const TileMask& mk) {
+  using Tile = SwzTile<D, BN>;
+  f32x4 s[2][2];
+  tile_scores<T, D, BN>(tK, lo, qf, kc, s);
+  float pv[2][8], ps[2];
+  Frag<T> pf[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) half_exp<true>(s, kc, qb, c2, m_run[qb], g, mk, pv[qb], ps[qb]);
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    if (__any(!(ps[qb] <= kSumMax))) half_rescale<D>(s, qb, c2, acc, m_run, l_run, pv[qb], ps[qb]);
+    l_run[qb] += ps[qb];
+    pf[qb] = pack8<T>(pv[qb]);
+  }
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    const char* pa = tV + (2 * kc) * Tile::kBlk16 + lo.v[db];
+    const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+    acc[db][0] = mma(acc[db][0], vt, pf[0]);
+    acc[db][1] = mma(acc[db][1], vt, pf[1]);
+  }
+}
+
 // NW waves of 32 queries share each K/V tile of BN = 64 rows (2 x 32 KB
 // double buffer at D = 128); at least 2 waves per SIMD. PH selects the key
 // phases (bit 0 local window, bit 1 global rows) at compile time, so the
@@ -497,10 +527,16 @@ void fwd2_kernel(FwdArgs a) {
       mk.span[qb] = loc ? (unsigned)(W - 1) : 0x7fffffffu;
     }
     if (work) {
+      // keys of the tile visible to some query of the wave: [vis_lo, vis_hi]
+      const int vis_lo = loc ? w_lo - ts : 0;
+      const int vis_hi = loc ? q_last - ts : wg_hi - 1 - ts;
+      const bool half0 = vis_lo <= 31, half1 = vis_hi >= 32;
       if (full)
         attend_tile2<T, D, BN, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
-      else
+      else if (half0 && half1)
         attend_tile2<T, D, BN, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
+      else
+        attend_half<T, D, BN>(tK, tV, half0 ? 0 : 1, lo, qf, acc, m_run, l_run, c2, g, mk);
     }
   };
   for (int it = 0; it < ntot; it += 2) {
