@@ -14,9 +14,10 @@
 //   2. dq_kernel         query-centric: local band + global prefix -> dQ
 //   3. dkdv_kernel<GLOB> packed global rows (strided + relay), query range
 //                        split in chunks -> fp32 partials in the workspace
+//   3b. gsum_kernel      sums the chunk partials of each global row
 //   4. dalpha_kernel     (optional) gradient of the relay log-scale
 //   5. dkdv_kernel<LOC>  key-centric local band; its epilogue adds the
-//                        chunk partials of the global rows whose source is
+//                        summed partials of the global rows whose source is
 //                        the key row (strided row r*W, relay source rows) and
 //                        writes dK/dV once.
 // No atomics: every output row has exactly one writer and the partial sums
@@ -527,15 +528,13 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
         }
       }
     }
+    // the chunk partials of the global rows are summed into chunk 0
     for (int m = 0; m < nm; ++m) {
-      for (int c = 0; c < a.nchunk; ++c) {
-        const float* pk =
-            a.gpart + (((int64_t)c * nbh + bhk) * a.G + dc.gofs + grow[m]) * 2 * D;
+      const float* pk = a.gpart + ((int64_t)bhk * a.G + dc.gofs + grow[m]) * 2 * D;
 #pragma unroll
-        for (int db = 0; db < Tr::kDB; ++db) {
-          dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
-          dva[db][kb] += *reinterpret_cast<const f32x4*>(pk + D + 16 * db + 4 * g) * gsc[m];
-        }
+      for (int db = 0; db < Tr::kDB; ++db) {
+        dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
+        dva[db][kb] += *reinterpret_cast<const f32x4*>(pk + D + 16 * db + 4 * g) * gsc[m];
       }
     }
 #pragma unroll
@@ -544,6 +543,26 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
       store4<T>(dvp + (int64_t)j * a.dvss + 16 * db + 4 * g, dva[db][kb], 1.f);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// 3b. Chunk partials of the global rows summed into chunk 0, in chunk order
+// (one float4 per thread; work items: the documents' rows x 2D / 4 / 256).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void gsum_kernel(BwdArgs a) {
+  constexpr int kVec = 2 * D / 4;  // float4 per row (dK and dV)
+  const int nbh = a.B * a.Hkv;
+  const int bhk = blockIdx.x % nbh;
+  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  const int rows = (dc.len + dc.W - 1) / dc.W * dc.rpb;
+  const int e = dc.item * 256 + (int)threadIdx.x;
+  if (e >= rows * kVec) return;
+  float* p0 = a.gpart + ((int64_t)bhk * a.G + dc.gofs) * 2 * D + 4 * (int64_t)e;
+  const int64_t cstride = (int64_t)nbh * a.G * 2 * D;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(p0);
+  for (int c = 1; c < a.nchunk; ++c) acc += *reinterpret_cast<const f32x4*>(p0 + c * cstride);
+  *reinterpret_cast<f32x4*>(p0) = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -567,12 +586,8 @@ __global__ __launch_bounds__(256) void dalpha_kernel(BwdArgs a) {
       for (int e = tid; e < nrel * D; e += 256) {
         const int t = e / D, d = e % D;
         const int row = a.docs.gofs[doc] + (t / a.top_k) * rpb + 1 + t % a.top_k;
-        float dk = 0.f, dv = 0.f;
-        for (int c = 0; c < a.nchunk; ++c) {
-          const float* pk = a.gpart + (((int64_t)c * nbh + bhk) * a.G + row) * 2 * D;
-          dk += pk[d];
-          dv += pk[D + d];
-        }
+        const float* pk = a.gpart + ((int64_t)bhk * a.G + row) * 2 * D;  // summed chunks
+        const float dk = pk[d], dv = pk[D + d];
         acc += dk * to_f32(gk[(int64_t)row * D + d]) + dv * to_f32(gv[(int64_t)row * D + d]);
       }
     }
@@ -1145,15 +1160,13 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
         }
       }
     }
+    // the chunk partials of the global rows are summed into chunk 0
     for (int m = 0; m < nm; ++m) {
-      for (int c = 0; c < a.nchunk; ++c) {
-        const float* pk =
-            a.gpart + (((int64_t)c * nbh + bhk) * a.G + dc.gofs + grow[m]) * 2 * D;
+      const float* pk = a.gpart + ((int64_t)bhk * a.G + dc.gofs + grow[m]) * 2 * D;
 #pragma unroll
-        for (int db = 0; db < D / 16; ++db) {
-          dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
-          dva[db][kb] += *reinterpret_cast<const f32x4*>(pk + D + 16 * db + 4 * g) * gsc[m];
-        }
+      for (int db = 0; db < D / 16; ++db) {
+        dka[db][kb] += *reinterpret_cast<const f32x4*>(pk + 16 * db + 4 * g) * gsc[m];
+        dva[db][kb] += *reinterpret_cast<const f32x4*>(pk + D + 16 * db + 4 * g) * gsc[m];
       }
     }
 #pragma unroll
@@ -1211,6 +1224,15 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((dq_kernel<T, D>), dim3(nq * a.B * a.Hq), dim3(256), 0, st, aq);
     hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(ng * a.B * a.Hkv), dim3(256), 0, st, ag);
   }
+  if (a.nchunk > 1) {
+    BwdArgs as = a;
+    set_items(as.docs, [&](int d) {
+      const int g = (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d] * a.docs.rpb[d];
+      return (g * (2 * D / 4) + 255) / 256;
+    });
+    hipLaunchKernelGGL((gsum_kernel<D>), dim3(as.docs.item0[a.docs.n] * a.B * a.Hkv), dim3(256),
+                       0, st, as);
+  }
   if (a.dalpha) hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (sizeof(T) == 2)
     hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvLocalWaves, kDkdvKB, kDkdvLocalBQ>),
@@ -1234,9 +1256,12 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
 
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
                            const int* W, const int* rpb, int64_t G, int* nchunk) {
-  // Enough global-row workgroups to cover the chip about twice: tiles of 128
-  // global rows per document and (b, kv head), each document's query range
-  // cut into the same number of chunks (multiples of 64 queries).
+  // About 2048 global-row workgroups (8 per CU): tiles of 128 global rows
+  // per document and (b, kv head), each document's query range cut into the
+  // same number of chunks (multiples of 64 queries). At B=1 H=16 D=128
+  // S=131072 that is 15 chunks; 8 and 22 measured 2% and 1% slower overall
+  // (the partial sums are reduced once by gsum_kernel, so more chunks only
+  // cost that kernel's reads).
   int64_t gtiles = 0;
   int max_len = 1;
   for (int d = 0; d < n; ++d) {
@@ -1245,7 +1270,7 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
     if (len[d] > max_len) max_len = len[d];
   }
   const int64_t base = gtiles * B * Hkv;
-  int64_t nc = (1024 + base - 1) / base;
+  int64_t nc = (2048 + base - 1) / base;
   const int64_t max_nc = (max_len + 255) / 256;
   if (nc > max_nc) nc = max_nc;
   if (nc < 1) nc = 1;
