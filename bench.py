@@ -176,6 +176,15 @@ def run_main(args):
     t_glob = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv,
                                                    phases=_native.PHASE_GLOBAL),
                            args.steps, args.warmup, torch)
+    # strided rows alone: the same global-phase kernel over packed rows built
+    # without relay (one row per block); the relay rows' share is the
+    # difference to the full global phase
+    p_s = _native.problem(B, H, H, S, D, W, False, 2, dtype, 1 / math.sqrt(D))
+    gk_s, gv_s, _ = _native.build_global(p_s, k, v, None)
+    t_str = per_launch_ms(lambda: _native.forward(p_s, q, k, v, gk_s, gv_s,
+                                                  phases=_native.PHASE_GLOBAL),
+                          args.steps, args.warmup, torch)
+    del gk_s, gv_s
     t_bg = per_launch_ms(lambda: _native.build_global(p, k, v, None), args.steps, args.warmup,
                          torch)
     G = int(_native.global_rows(p))
@@ -184,6 +193,9 @@ def run_main(args):
     bg_bytes = B * H * (S * D * e + G * D * e + 2 * G * D * e + 4 * NB * 2)
     f_loc = 4 * D * pp["local"] * B * H
     f_glob = 4 * D * (pp["strided"] + pp["relay"]) * B * H
+    f_str = 4 * D * pp["strided"] * B * H
+    f_rel = 4 * D * pp["relay"] * B * H
+    t_rel = t_glob - t_str
     phases = {
         "local": {"ms": round(t_loc, 4), "pairs_per_head": pp["local"],
                   "tflops": round(f_loc / (t_loc * 1e-3) / 1e12, 2),
@@ -193,6 +205,15 @@ def run_main(args):
                    "strided_pairs_per_head": pp["strided"], "relay_pairs_per_head": pp["relay"],
                    "tflops": round(f_glob / (t_glob * 1e-3) / 1e12, 2),
                    "mfma_frac": round(f_glob / (t_glob * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
+        "strided": {"ms": round(t_str, 4), "pairs_per_head": pp["strided"],
+                    "tflops": round(f_str / (t_str * 1e-3) / 1e12, 2),
+                    "mfma_frac": round(f_str / (t_str * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                    "how": "global phase over strided rows only (relay off)"},
+        "relay": {"ms": round(t_rel, 4), "pairs_per_head": pp["relay"],
+                  "tflops": round(f_rel / (t_rel * 1e-3) / 1e12, 2) if t_rel > 0 else None,
+                  "mfma_frac": (round(f_rel / (t_rel * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
+                                if t_rel > 0 else None),
+                  "how": "global phase minus strided-only"},
         "build_global": {"ms": round(t_bg, 4), "bytes": bg_bytes,
                          "GBps": round(bg_bytes / (t_bg * 1e-3) / 1e9, 1),
                          "hbm_frac": round(bg_bytes / (t_bg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},

@@ -82,7 +82,7 @@ struct BwdArgs {
   void* dk;
   void* dv;
   float* delta;    // [B, Hq, S] rowsum(o * do)
-  float* gpart;    // [nchunk, B, Hq, G, 2, D] fp32 partial dK/dV of the global rows
+  float* gpart;    // [nchunk, B, Hkv, G, 2, D] fp32 partial dK/dV of the global rows
   float* dalpha;   // [Hkv] or null
   int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, osb, osh, oss;
   int64_t dosb, dosh, doss, dqsb, dqsh, dqss, dksb, dksh, dkss, dvsb, dvsh, dvss;
@@ -92,7 +92,7 @@ struct BwdArgs {
   int64_t G;       // packed global rows of all documents, per head
   float scale;
   int nchunk;      // query chunks per document of the global-row kernel
-  int group;       // 0: first launch of a call (computes Delta, writes dalpha);
+  int group;       // 0: first launch of a call (fp32: computes Delta; writes dalpha);
                    // later document groups of the call add to dalpha
   Docs docs;       // items: set by the launcher per kernel
 };
