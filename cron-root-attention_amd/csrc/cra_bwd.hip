@@ -433,6 +433,9 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
     q_hi = c_hi;
     wq_lo = active ? max(c_lo, glob_row_first_query(kw, W, rpb)) : S;
     wq_hi = c_hi;
+    // no query of this chunk sees the tile's rows: gsum_kernel skips the
+    // chunk for them (with a single chunk the zeros are written instead)
+    if (q_hi <= q_lo && a.nchunk > 1) return;
   } else {
     q_lo = k0;
     q_hi = min(S, k0 + Tr::kBK - 1 + W);
@@ -548,6 +551,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // 3b. Chunk partials of the global rows summed into chunk 0, in chunk order
 // (one float4 per thread; work items: the documents' rows x 2D / 4 / 256).
+// Only chunks with a query that sees the row are read.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void gsum_kernel(BwdArgs a) {
@@ -558,10 +562,17 @@ __global__ __launch_bounds__(256) void gsum_kernel(BwdArgs a) {
   const int rows = (dc.len + dc.W - 1) / dc.W * dc.rpb;
   const int e = dc.item * 256 + (int)threadIdx.x;
   if (e >= rows * kVec) return;
+  // Chunks [c_lo, c_hi) hold queries that see the row; the global-row
+  // kernel wrote no partial for the others (their workgroups had no query
+  // that sees the tile), so they are skipped rather than read.
+  const int L = chunk_len_for(dc.len, a.nchunk);
+  const int first = glob_row_first_query(e / kVec, dc.W, dc.rpb);
+  const int c_lo = first / L;
+  const int c_hi = first < dc.len ? min(a.nchunk, (dc.len + L - 1) / L) : c_lo;
   float* p0 = a.gpart + ((int64_t)bhk * a.G + dc.gofs) * 2 * D + 4 * (int64_t)e;
   const int64_t cstride = (int64_t)nbh * a.G * 2 * D;
-  f32x4 acc = *reinterpret_cast<const f32x4*>(p0);
-  for (int c = 1; c < a.nchunk; ++c) acc += *reinterpret_cast<const f32x4*>(p0 + c * cstride);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = c_lo; c < c_hi; ++c) acc += *reinterpret_cast<const f32x4*>(p0 + c * cstride);
   *reinterpret_cast<f32x4*>(p0) = acc;
 }
 
@@ -998,6 +1009,9 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
     const int c_lo = chunk * chunk_len;
     q_hi = min(S, c_lo + chunk_len);
     q_lo = max(c_lo, glob_row_first_query(k0, W, rpb));
+    // no query of this chunk sees the tile's rows: gsum_kernel skips the
+    // chunk for them (with a single chunk the zeros are written instead)
+    if (q_hi <= q_lo && a.nchunk > 1) return;
   } else {
     q_lo = k0;
     q_hi = min(S, k0 + kBK - 1 + W);
