@@ -6,6 +6,8 @@ forward + backward of the attention op (o = attn(q, k, v); o.backward(dO)).
 Prints ONE JSON line:
   value        whole-job effective TFLOP/s of fwd+bwd (14*D*pairs / time)
   fwd_ms / fwdbwd_ms and their effective TFLOP/s
+  fwdbwd_per_step  10% trimmed mean, coefficient of variation, min and max of
+               the same step timed one call at a time
   roofline     the forward kernel (one launch of cra_fwd = one kernel), timed
                with HIP events on the stream it runs on, against the fp16
                dense MFMA peak; traffic from a committed rocprofv3 --pmc
@@ -79,6 +81,30 @@ def timed(fn, steps, warmup, torch):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def per_step_ms(fn, steps, torch):
+    """Each of `steps` calls bracketed by its own events (no warmup: call
+    after `timed`); returns the list of per-call milliseconds."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return [e0.elapsed_time(e1) for e0, e1 in ev]
+
+
+def spread(ms):
+    """10% trimmed mean and coefficient of variation of per-step times."""
+    xs = sorted(ms)
+    k = len(xs) // 10
+    core = xs[k:len(xs) - k] if len(xs) > 2 * k else xs
+    mean = sum(xs) / len(xs)
+    var = sum((x - mean) ** 2 for x in xs) / max(1, len(xs) - 1)
+    return {"n": len(xs), "trimmed_mean_ms": round(sum(core) / len(core), 4),
+            "cov": round(var ** 0.5 / mean, 4), "min_ms": round(xs[0], 4), "max_ms": round(xs[-1], 4)}
 
 
 def per_launch_ms(fn, steps, warmup, torch):
@@ -155,6 +181,8 @@ def run_main(args):
         cra.cron_root_attention(qg, kg, vg).backward(dO)
 
     step_ms = timed(step, args.steps, args.warmup, torch)
+    # per-step spread of the same step (reported beside the bracketed mean)
+    per_step = per_step_ms(step, max(args.steps, 10), torch)
 
     # forward kernel alone: cra_fwd launches exactly one kernel
     W = int(math.ceil(math.sqrt(S)))
@@ -233,7 +261,8 @@ def run_main(args):
                    "B": B, "H": H, "S": S, "D": D, "window": W, "relay_top_k": 2},
         "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 3),
         "fwdbwd_ms": round(step_ms, 4), "fwdbwd_tflops": round(f_all / (step_ms * 1e-3) / 1e12, 3),
-        "pairs_per_head": P, "roofline": roof, "phases": phases, "cpu_baseline": cpu,
+        "pairs_per_head": P, "fwdbwd_per_step": spread(per_step),
+        "roofline": roof, "phases": phases, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 
@@ -343,8 +372,8 @@ def run_crossover(args):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=16)
