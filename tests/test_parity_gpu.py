@@ -328,3 +328,31 @@ def test_ns_backward_identities_and_determinism():
     sdk = dk.double().sum(2)
     assert float(sdk.abs().max()) <= 1e-2 * float(dk.double().abs().sum(2).max())
     assert torch.isfinite(dq).all() and torch.isfinite(dk).all() and torch.isfinite(dv).all()
+
+
+@pytest.mark.parametrize("B,H,S,dtype,bwd", [(1, 16, 524288, F16, True), (2, 32, 262144, BF16, False)])
+def test_largest_baseline_shapes(B, H, S, dtype, bwd):
+    """BASELINE's largest configurations (config 3 at S=524288 with the
+    backward, config 5 at S=262144): finite outputs and gradients, and the
+    last 64 rows of head 0 against the oracle."""
+    say(f"large shape B={B} H={H} S={S} {dtype} bwd={bwd}")
+    D = 128
+    g = torch.Generator(device=DEV).manual_seed(0)
+    mk = lambda: torch.randn(B, H, S, D, generator=g, device=DEV, dtype=torch.float32).to(dtype)
+    q, k, v = mk(), mk(), mk()
+    if bwd:
+        qg, kg, vg = (t.requires_grad_(True) for t in (q, k, v))
+        o = cra.cron_root_attention(qg, kg, vg)
+        o.backward(mk())
+        for t in (o, qg.grad, kg.grad, vg.grad):
+            assert bool(torch.isfinite(t).all())
+    else:
+        with torch.no_grad():
+            o = cra.cron_root_attention(q, k, v)
+        assert bool(torch.isfinite(o).all())
+    rows = (S - 64, S)
+    qc, kc, vc = (t[:1, :1].detach().float().cpu() for t in (q, k, v))
+    ref, _, _ = O.forward(qc, kc, vc, plan_for(S), rows=rows)
+    err = max_abs(o[:1, :1, rows[0]:rows[1]], ref)
+    say(f"  last 64 rows: max err {err:.2e}")
+    assert err <= TOL_FWD[dtype]
