@@ -49,41 +49,47 @@ __global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
     const int nrows = min(W, dc.len - row0);
     float bn[4] = {kSentinel, kSentinel, kSentinel, kSentinel};
     int bi[4] = {0, 0, 0, 0};
-    for (int base = 0; base < nrows; base += kNRG) {  // uniform trip count
-      const int rr = base + rg;
-      const bool valid = rr < nrows;
-      float x[8];
-      if (valid) {
+    // kU row groups per pass: their loads are issued together (rows past the
+    // block are clamped to its last row and left out of the ranking), then
+    // the norms are ranked in row order
+    constexpr int kU = 8;
+    for (int base = 0; base < nrows; base += kU * kNRG) {  // uniform trip count
+      uint4 w[kU][kW16];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int rr = min(base + u * kNRG + rg, nrows - 1);
         const uint4* p = reinterpret_cast<const uint4*>(kb + (int64_t)(row0 + rr) * a.kss + li * 8);
-        uint4 w[kW16];
 #pragma unroll
-        for (int i = 0; i < kW16; ++i) w[i] = p[i];
-        const T* e = reinterpret_cast<const T*>(w);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = to_f32(e[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = 0.f;
+        for (int i = 0; i < kW16; ++i) w[u][i] = p[i];
       }
-      float acc = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc = __fadd_rn(acc, __fmul_rn(x[i], x[i]));
+      for (int u = 0; u < kU; ++u) {
+        const int rr = base + u * kNRG + rg;
+        const bool valid = rr < nrows;
+        const T* e = reinterpret_cast<const T*>(w[u]);
+        float acc = 0.f;
 #pragma unroll
-      for (int off = kLPR / 2; off >= 1; off >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, off));
-      if (valid) {
-        // strict '>' cascade, rows arrive in increasing order within a group
-        const bool b0 = acc > bn[0], b1 = acc > bn[1], b2 = acc > bn[2], b3 = acc > bn[3];
-        const float n3 = b2 ? bn[2] : (b3 ? acc : bn[3]);
-        const int i3 = b2 ? bi[2] : (b3 ? rr : bi[3]);
-        const float n2 = b1 ? bn[1] : (b2 ? acc : bn[2]);
-        const int i2 = b1 ? bi[1] : (b2 ? rr : bi[2]);
-        const float n1 = b0 ? bn[0] : (b1 ? acc : bn[1]);
-        const int i1 = b0 ? bi[0] : (b1 ? rr : bi[1]);
-        bn[0] = b0 ? acc : bn[0];
-        bi[0] = b0 ? rr : bi[0];
-        bn[1] = n1; bi[1] = i1;
-        bn[2] = n2; bi[2] = i2;
-        bn[3] = n3; bi[3] = i3;
+        for (int i = 0; i < 8; ++i) {
+          const float x = to_f32(e[i]);
+          acc = __fadd_rn(acc, __fmul_rn(x, x));
+        }
+#pragma unroll
+        for (int off = kLPR / 2; off >= 1; off >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, off));
+        if (valid) {
+          // strict '>' cascade, rows arrive in increasing order within a group
+          const bool b0 = acc > bn[0], b1 = acc > bn[1], b2 = acc > bn[2], b3 = acc > bn[3];
+          const float n3 = b2 ? bn[2] : (b3 ? acc : bn[3]);
+          const int i3 = b2 ? bi[2] : (b3 ? rr : bi[3]);
+          const float n2 = b1 ? bn[1] : (b2 ? acc : bn[2]);
+          const int i2 = b1 ? bi[1] : (b2 ? rr : bi[2]);
+          const float n1 = b0 ? bn[0] : (b1 ? acc : bn[1]);
+          const int i1 = b0 ? bi[0] : (b1 ? rr : bi[1]);
+          bn[0] = b0 ? acc : bn[0];
+          bi[0] = b0 ? rr : bi[0];
+          bn[1] = n1; bi[1] = i1;
+          bn[2] = n2; bi[2] = i2;
+          bn[3] = n3; bi[3] = i3;
+        }
       }
     }
     if (li == 0) {
