@@ -771,26 +771,34 @@ void dq2_kernel(BwdArgs a) {
   // for the dK/dV kernels: lane (l16, g) sums its 32 columns, then the four
   // lanes of a query add theirs in a fixed order.
   const T* opp = static_cast<const T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
+  // All of the wave's Q, dO and O fragments are loaded before any is used
+  // (rows past the document read its last row: those queries' results are
+  // never stored), so the loads are in flight together.
+  Frag<T> of[QB][D / 32];
+  float lv[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
+    const int qr = min(qi[qb], S - 1);
+    lv[qb] = lse[qr];
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c) {
+      qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qr * a.qss + 32 * c + 8 * g);
+      df[qb][c] = lds_frag_row<T>(dop + (int64_t)qr * a.doss + 32 * c + 8 * g);
+      of[qb][c] = lds_frag_row<T>(opp + (int64_t)qr * a.oss + 32 * c + 8 * g);
+    }
+  }
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
     const bool ok = qi[qb] < S;
-    lse2[qb] = ok ? lse[qi[qb]] * kLog2e : 0.f;
+    lse2[qb] = ok ? lv[qb] * kLog2e : 0.f;
     float od = 0.f;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) {
-      if (ok) {
-        qf[qb][c] = lds_frag_row<T>(qp + (int64_t)qi[qb] * a.qss + 32 * c + 8 * g);
-        df[qb][c] = lds_frag_row<T>(dop + (int64_t)qi[qb] * a.doss + 32 * c + 8 * g);
-        const Frag<T> of = lds_frag_row<T>(opp + (int64_t)qi[qb] * a.oss + 32 * c + 8 * g);
-        const T* eo = reinterpret_cast<const T*>(of.w);
-        const T* ed = reinterpret_cast<const T*>(df[qb][c].w);
+      const T* eo = reinterpret_cast<const T*>(of[qb][c].w);
+      const T* ed = reinterpret_cast<const T*>(df[qb][c].w);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) od = fmaf(to_f32(eo[i]), to_f32(ed[i]), od);
-      } else {
-        zero_frag(qf[qb][c]);
-        zero_frag(df[qb][c]);
-      }
+      for (int i = 0; i < 8; ++i) od = fmaf(to_f32(eo[i]), to_f32(ed[i]), od);
     }
     od += __shfl_xor(od, 16);
     od += __shfl_xor(od, 32);
