@@ -884,21 +884,28 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
   using Tile = SwzTile<D, BQ>;
   constexpr int NS = BQ / 32;  // 32-query subtiles
   // S = Q . K^T and dP = dO . V^T of subtile qs (two 16-query blocks)
+  // Fragments are read one step ahead of the MFMAs that use them.
   auto scores = [&](int qs, f32x4 (&sc)[2][KB], f32x4 (&dp)[2][KB]) {
+    constexpr int NC = D / 32;
+    Frag<T> qa[2], oa[2];
+    qa[0] = Tile::template row_frag_at<T>(tQ + (2 * qs) * Tile::kBlk16 + lo.row[0]);
+    oa[0] = Tile::template row_frag_at<T>(tO + (2 * qs) * Tile::kBlk16 + lo.row[0]);
 #pragma unroll
-    for (int qb2 = 0; qb2 < 2; ++qb2) {
-      const int qblk = 2 * qs + qb2;
+    for (int qb2 = 0; qb2 < 2; ++qb2)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) sc[qb2][kb] = dp[qb2][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        const Frag<T> qa = Tile::template row_frag_at<T>(tQ + qblk * Tile::kBlk16 + lo.row[c]);
-        const Frag<T> oa = Tile::template row_frag_at<T>(tO + qblk * Tile::kBlk16 + lo.row[c]);
+    for (int t = 0; t < 2 * NC; ++t) {
+      const int qb2 = t / NC, c = t % NC;
+      if (t + 1 < 2 * NC) {
+        const int qn = 2 * qs + (t + 1) / NC, cn = (t + 1) % NC;
+        qa[(t + 1) & 1] = Tile::template row_frag_at<T>(tQ + qn * Tile::kBlk16 + lo.row[cn]);
+        oa[(t + 1) & 1] = Tile::template row_frag_at<T>(tO + qn * Tile::kBlk16 + lo.row[cn]);
+      }
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          sc[qb2][kb] = mma(sc[qb2][kb], qa, kf[kb][c]);
-          dp[qb2][kb] = mma(dp[qb2][kb], oa, vf[kb][c]);
-        }
+      for (int kb = 0; kb < KB; ++kb) {
+        sc[qb2][kb] = mma(sc[qb2][kb], qa[t & 1], kf[kb][c]);
+        dp[qb2][kb] = mma(dp[qb2][kb], oa[t & 1], vf[kb][c]);
       }
     }
   };
@@ -950,14 +957,19 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
                            ds[1][kb][0], ds[1][kb][1], ds[1][kb][2], ds[1][kb][3]};
       const Frag<T> pf = pack8<T>(pv);
       const Frag<T> sf = pack8<T>(sv);
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
+      Frag<T> ot[2], qt[2];
+      auto tr_pair = [&](int db, Frag<T>& o_, Frag<T>& q_) {
         const char* po = tO + (2 * qs) * Tile::kBlk16 + lo.tr[db];
         const char* pq = tQ + (2 * qs) * Tile::kBlk16 + lo.tr[db];
-        const Frag<T> ot = Tile::template tr_frag_at<T>(po, po + Tile::kBlk16);
-        const Frag<T> qt = Tile::template tr_frag_at<T>(pq, pq + Tile::kBlk16);
-        dva[db][kb] = mma(dva[db][kb], ot, pf);
-        dka[db][kb] = mma(dka[db][kb], qt, sf);
+        o_ = Tile::template tr_frag_at<T>(po, po + Tile::kBlk16);
+        q_ = Tile::template tr_frag_at<T>(pq, pq + Tile::kBlk16);
+      };
+      tr_pair(0, ot[0], qt[0]);
+#pragma unroll
+      for (int db = 0; db < D / 16; ++db) {
+        if (db + 1 < D / 16) tr_pair(db + 1, ot[(db + 1) & 1], qt[(db + 1) & 1]);
+        dva[db][kb] = mma(dva[db][kb], ot[db & 1], pf);
+        dka[db][kb] = mma(dka[db][kb], qt[db & 1], sf);
       }
     }
   }
