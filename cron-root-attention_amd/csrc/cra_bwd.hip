@@ -649,27 +649,36 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
                                          const float (&dl)[QB], float c2, int g,
                                          const TileMask& mk, bool half0, bool half1) {
   using Tile = SwzTile<D, 64>;
+  constexpr int NC = D / 32;
 #pragma unroll
   for (int kc = 0; kc < 2; ++kc) {
     // masked tiles: a 32-key half with no key visible to the wave is skipped
     if (MASK && !(kc ? half1 : half0)) continue;
     float ds[2][QB][4];  // [h][qb][r]
+    // K and V row fragments are read one step ahead of their MFMAs
+    Frag<T> kf[2], vf[2];
+    kf[0] = Tile::template row_frag_at<T>(tK + (2 * kc) * Tile::kBlk16 + lo.row[0]);
+    vf[0] = Tile::template row_frag_at<T>(tV + (2 * kc) * Tile::kBlk16 + lo.row[0]);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int kb = 2 * kc + h;
       f32x4 sc[QB], dp[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) sc[qb] = dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.row[c]);
-        const Frag<T> vf = Tile::template row_frag_at<T>(tV + kb * Tile::kBlk16 + lo.row[c]);
+      for (int c = 0; c < NC; ++c) {
+        const int t = h * NC + c;
+        if (t + 1 < 2 * NC) {
+          const int kn = 2 * kc + (t + 1) / NC, cn = (t + 1) % NC;
+          kf[(t + 1) & 1] = Tile::template row_frag_at<T>(tK + kn * Tile::kBlk16 + lo.row[cn]);
+          vf[(t + 1) & 1] = Tile::template row_frag_at<T>(tV + kn * Tile::kBlk16 + lo.row[cn]);
+        }
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-          sc[qb] = mma(sc[qb], kf, qf[qb][c]);
-          dp[qb] = mma(dp[qb], vf, df[qb][c]);
+          sc[qb] = mma(sc[qb], kf[t & 1], qf[qb][c]);
+          dp[qb] = mma(dp[qb], vf[t & 1], df[qb][c]);
         }
       }
+      const int kb = 2 * kc + h;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int ko = 16 * kb + 4 * g + r;
@@ -688,12 +697,18 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
                            ds[1][qb][0], ds[1][qb][1], ds[1][qb][2], ds[1][qb][3]};
       dsf[qb] = pack8<T>(v8);
     }
+    // transposed K fragments, also one step ahead
+    Frag<T> kt[2];
+    auto tr_k = [&](int db) {
+      const char* pa = tK + (2 * kc) * Tile::kBlk16 + lo.tr[db];
+      return Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+    };
+    kt[0] = tr_k(0);
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-      const char* pa = tK + (2 * kc) * Tile::kBlk16 + lo.tr[db];
-      const Frag<T> kt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+      if (db + 1 < D / 16) kt[(db + 1) & 1] = tr_k(db + 1);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) dqa[db][qb] = mma(dqa[db][qb], kt, dsf[qb]);
+      for (int qb = 0; qb < QB; ++qb) dqa[db][qb] = mma(dqa[db][qb], kt[db & 1], dsf[qb]);
     }
   }
 }
