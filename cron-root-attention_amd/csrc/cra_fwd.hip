@@ -262,17 +262,43 @@ __device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& l
                                             const Frag<T> (&qf)[2][D / 32], int kc,
                                             f32x4 (&s)[2][2]) {
   using Tile = SwzTile<D, BN>;
+  constexpr int NC = D / 32;
+  // K fragments are read one step ahead of the MFMAs that use them
+  Frag<T> kf[2];
+  kf[0] = Tile::template row_frag_at<T>(tK + (2 * kc) * Tile::kBlk16 + lo.k[0]);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int kb = 2 * kc + h;
     s[h][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[h][1] = s[h][0];
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-      const Frag<T> kf = Tile::template row_frag_at<T>(tK + kb * Tile::kBlk16 + lo.k[c]);
-      s[h][0] = mma(s[h][0], kf, qf[0][c]);
-      s[h][1] = mma(s[h][1], kf, qf[1][c]);
+    for (int c = 0; c < NC; ++c) {
+      const int t = h * NC + c;
+      if (t + 1 < 2 * NC)
+        kf[(t + 1) & 1] = Tile::template row_frag_at<T>(
+            tK + (2 * kc + (t + 1) / NC) * Tile::kBlk16 + lo.k[(t + 1) % NC]);
+      s[h][0] = mma(s[h][0], kf[t & 1], qf[0][c]);
+      s[h][1] = mma(s[h][1], kf[t & 1], qf[1][c]);
     }
+  }
+}
+
+// O^T += V^T . P^T for 32-key half kh: transposed V fragments read one step
+// ahead of the MFMAs that use them.
+template <typename T, int D, int BN>
+__device__ __forceinline__ void pv_half(const char* tV, int kh, const Fwd2Lane<D>& lo,
+                                        const Frag<T> (&pf)[2], f32x4 (&acc)[D / 16][2]) {
+  using Tile = SwzTile<D, BN>;
+  auto tr_v = [&](int db) {
+    const char* pa = tV + (2 * kh) * Tile::kBlk16 + lo.v[db];
+    return Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
+  };
+  Frag<T> vt[2];
+  vt[0] = tr_v(0);
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db) {
+    if (db + 1 < D / 16) vt[(db + 1) & 1] = tr_v(db + 1);
+    acc[db][0] = mma(acc[db][0], vt[db & 1], pf[0]);
+    acc[db][1] = mma(acc[db][1], vt[db & 1], pf[1]);
   }
 }
 
@@ -346,16 +372,7 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
       half_exp<MASK>(s[kc], kc, qb, c2, m_run[qb], g, mk, pv[qb], ps[qb]);
-    if (kc > 0) {
-      // PV of the previous half, beside this half's exponentials
-#pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
-        const char* pa = tV + (2 * (kc - 1)) * Tile::kBlk16 + lo.v[db];
-        const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
-        acc[db][0] = mma(acc[db][0], vt, pf[0]);
-        acc[db][1] = mma(acc[db][1], vt, pf[1]);
-      }
-    }
+    if (kc > 0) pv_half<T, D, BN>(tV, kc - 1, lo, pf, acc);  // beside this half's exponentials
     if (kc + 1 < kHalves) tile_scores<T, D, BN>(tK, lo, qf, kc + 1, s[kc + 1]);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
@@ -365,13 +382,7 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
       pf[qb] = pack8<T>(pv[qb]);
     }
   }
-#pragma unroll
-  for (int db = 0; db < D / 16; ++db) {
-    const char* pa = tV + (2 * (kHalves - 1)) * Tile::kBlk16 + lo.v[db];
-    const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
-    acc[db][0] = mma(acc[db][0], vt, pf[0]);
-    acc[db][1] = mma(acc[db][1], vt, pf[1]);
-  }
+  pv_half<T, D, BN>(tV, kHalves - 1, lo, pf, acc);
 }
 
 // One 32-key half kc of a masked tile, for tiles whose other half has no
@@ -395,13 +406,7 @@ __device__ __forceinline__ void attend_half(const char* tK, const char* tV, int 
     l_run[qb] += ps[qb];
     pf[qb] = pack8<T>(pv[qb]);
   }
-#pragma unroll
-  for (int db = 0; db < D / 16; ++db) {
-    const char* pa = tV + (2 * kc) * Tile::kBlk16 + lo.v[db];
-    const Frag<T> vt = Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
-    acc[db][0] = mma(acc[db][0], vt, pf[0]);
-    acc[db][1] = mma(acc[db][1], vt, pf[1]);
-  }
+  pv_half<T, D, BN>(tV, kc, lo, pf, acc);
 }
 
 // NW waves of 32 queries share each K/V tile of BN = 64 rows (2 x 32 KB
