@@ -753,7 +753,9 @@ void dq2_kernel(BwdArgs a) {
   const int hi = min(S, m0 + kBM);
   const int gmax = glob_prefix(hi - 1, W, rpb);
   const int nloc = (hi - lo_k + kBN - 1) / kBN;
-  const int ntot = nloc + (gmax + kBN - 1) / kBN;
+  // global tiles first: their first fill is an L2 hit (see fwd2_kernel)
+  const int nglob = (gmax + kBN - 1) / kBN;
+  const int ntot = nloc + nglob;
   // Buffer resources over the rows this workgroup may read (local rows below
   // hi, global rows below gmax): loads past them return zeros.
   using Fill = typename Tile::template Fill<NW>;
@@ -766,12 +768,12 @@ void dq2_kernel(BwdArgs a) {
   const int fv = Fill::lane_off(wave, lane, vbytes);
   const int fg = Fill::lane_off(wave, lane, D * 2);
   auto issue = [&](int it, char* dst) {
-    if (it < nloc) {
-      const int ts = lo_k + it * kBN;
+    if (it >= nglob) {
+      const int ts = lo_k + (it - nglob) * kBN;
       Fill::load(dst, rk, fk, kbytes, ts, wave);
       Fill::load(dst + Tile::kBytes, rv, fv, vbytes, ts, wave);
     } else {
-      const int ts = (it - nloc) * kBN;
+      const int ts = it * kBN;
       Fill::load(dst, rgk, fg, D * 2, ts, wave);
       Fill::load(dst + Tile::kBytes, rgv, fg, D * 2, ts, wave);
     }
@@ -847,8 +849,8 @@ void dq2_kernel(BwdArgs a) {
     if (it + 1 < ntot) issue(it + 1, nxt[0]);
     const char* tK = cur[0];
     const char* tV = cur[1];
-    const bool loc = it < nloc;
-    const int ts = loc ? lo_k + it * kBN : (it - nloc) * kBN;
+    const bool loc = it >= nglob;
+    const int ts = loc ? lo_k + (it - nglob) * kBN : it * kBN;
     const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
     const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
     TileMask mk;
