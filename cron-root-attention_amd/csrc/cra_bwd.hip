@@ -1323,12 +1323,14 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
 
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
                            const int* W, const int* rpb, int64_t G, int* nchunk) {
-  // About 2048 global-row workgroups (8 per CU): tiles of 128 global rows
+  // About 3072 global-row workgroups (12 per CU): tiles of 128 global rows
   // per document and (b, kv head), each document's query range cut into the
-  // same number of chunks (multiples of 64 queries). At B=1 H=16 D=128
-  // S=131072 that is 15 chunks; 8 and 22 measured 2% and 1% slower overall
-  // (the partial sums are reduced once by gsum_kernel, so more chunks only
-  // cost that kernel's reads).
+  // same number of chunks (multiples of 64 queries). The global-row kernel
+  // runs one workgroup per CU, so its chunks are long jobs and the last
+  // round leaves CUs idle; more chunks shorten that tail at the cost of
+  // more partial sums (written once, reduced once by gsum_kernel). At B=1
+  // H=16 D=128 S=131072 that is 22 chunks; 15 and 29 measured 0.8% and
+  // 0.1% slower backward.
   int64_t gtiles = 0;
   int max_len = 1;
   for (int d = 0; d < n; ++d) {
@@ -1337,7 +1339,7 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
     if (len[d] > max_len) max_len = len[d];
   }
   const int64_t base = gtiles * B * Hkv;
-  int64_t nc = (2048 + base - 1) / base;
+  int64_t nc = (3072 + base - 1) / base;
   const int64_t max_nc = (max_len + 255) / 256;
   if (nc > max_nc) nc = max_nc;
   if (nc < 1) nc = 1;
