@@ -1057,9 +1057,11 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
   const int ntot = ntile_q * grp;
 
   const int qbytes = (int)(a.qss * 2), obytes = (int)(a.doss * 2);
-  using Fill = typename Tile::template Fill<NW>;
-  const int fq = Fill::lane_off(wave, lane, qbytes);
-  const int fo = Fill::lane_off(wave, lane, obytes);
+  // the first FW (a power of two) waves fill the tiles
+  constexpr int FW = NW >= 8 ? 8 : NW;
+  using Fill = typename Tile::template Fill<FW>;
+  const int fq = Fill::lane_off(wave & (FW - 1), lane, qbytes);
+  const int fo = Fill::lane_off(wave & (FW - 1), lane, obytes);
 
   const LaneOffs<D> lo = lane_offs<D>(lane);
   Frag<T> kf[KB][D / 32], vf[KB][D / 32];
@@ -1132,8 +1134,10 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
   int ld_j = 0, ld_t = 0;  // next tile to load
   auto load_tile = [&](char (&dst)[2][Tile::kBytes], float (&dsl)[2][kBQ]) {
     const int ts = q_lo + ld_t * kBQ;
-    Fill::load(dst[0], ld_res.q, fq, qbytes, ts, wave);
-    Fill::load(dst[1], ld_res.o, fo, obytes, ts, wave);
+    if (NW == FW || wave < FW) {
+      Fill::load(dst[0], ld_res.q, fq, qbytes, ts, wave);
+      Fill::load(dst[1], ld_res.o, fo, obytes, ts, wave);
+    }
     // one lane per query row of the tile (lane i of pass c lands at
     // dsl[.][64 c + i])
     if (wave == 0) {
@@ -1246,12 +1250,15 @@ __global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
 
 // dK/dV workgroups: waves of 16 key rows (no register file spill into AGPR
 // copies at D = 128; 32 rows per wave measured 14% slower). The global-row
-// kernel uses 8 waves (128 rows; 4 waves measured 3% slower); the local
+// kernel uses 12 waves (192 rows): at 160 VGPRs a SIMD holds 3 of its
+// waves, and one 12-wave workgroup fills them, where a second 8-wave
+// workgroup did not fit beside the first (8 waves measured 1.7% slower
+// backward, 4 waves 3% slower than 8); the local
 // kernel 4 waves (64 rows: its band of queries, 64 + W - 1, wastes fewer
 // pairs than with 128 rows; measured 7% faster). dQ workgroups: 4 waves of
 // 32 queries (each K/V fragment read from LDS serves two query blocks; 8
 // waves of 16 queries measured 27% slower at D = 128).
-constexpr int kDkdvGlobWaves = 8;
+constexpr int kDkdvGlobWaves = 12;
 constexpr int kDkdvLocalWaves = 4;
 constexpr int kDkdvKB = 1;  // 16-key blocks per wave
 constexpr int kDqWaves = 4;
@@ -1323,9 +1330,10 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
 
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
                            const int* W, const int* rpb, int64_t G, int* nchunk) {
-  // About 3072 global-row workgroups (12 per CU): tiles of 128 global rows
-  // per document and (b, kv head), each document's query range cut into the
-  // same number of chunks (multiples of 64 queries). The global-row kernel
+  // About 3072 tiles of 128 global rows (2112 workgroups of the global-row
+  // kernel's 192 rows at the shape below), per document and (b, kv head):
+  // each document's query range cut into the same number of chunks
+  // (multiples of 64 queries). The global-row kernel
   // runs one workgroup per CU, so its chunks are long jobs and the last
   // round leaves CUs idle; more chunks shorten that tail at the cost of
   // more partial sums (written once, reduced once by gsum_kernel). At B=1
