@@ -926,18 +926,16 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
       }
     }
   };
-  // LOC (local rows): software pipeline over the subtiles, the next
-  // subtile's score MFMAs beside this subtile's exponentials in program
-  // order (4% faster), and masks as one unsigned compare (within 1%). The
-  // global-row kernel compiles either change to 224-238 VGPRs and runs 6-7%
-  // slower, so it keeps scores and exponentials in sequence and two
-  // compares.
-  f32x4 sc[2][2][KB], dp[2][2][KB];  // [buffer][qb2][kb]
-  if (LOC) scores(0, sc[0], dp[0]);
+  // Each subtile's scores, then its exponentials, in sequence: 160 VGPRs,
+  // 3 waves per SIMD. (A software pipeline over the subtiles, the next
+  // subtile's score MFMAs beside this one's exponentials, needs 225
+  // registers and 2 waves per SIMD: 4.2% slower backward with the local
+  // kernel.) LOC (local rows) tests each mask with one unsigned compare;
+  // the global-row kernel keeps two compares.
+  f32x4 sc[2][KB], dp[2][KB];  // [qb2][kb]
 #pragma unroll
   for (int qs = 0; qs < NS; ++qs) {
-    const int cur = LOC ? (qs & 1) : 0;
-    if (!LOC) scores(qs, sc[0], dp[0]);
+    scores(qs, sc, dp);
     float p[2][KB][4], ds[2][KB][4];  // [qb2][kb][r]
     // query 16 qblk + 4g + r of the tile is visible to key kb iff
     // (unsigned)(16 qblk + r - q0[kb]) <= qspan[kb]
@@ -953,7 +951,7 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          float x = fmaf(sc[cur][qb2][kb][r], c2, -lq[r]);
+          float x = fmaf(sc[qb2][kb][r], c2, -lq[r]);
           if (MASK) {
             const bool out = LOC ? (unsigned)(16 * qblk + r - q0[kb]) > qspan[kb]
                                  : (ts + 16 * qblk + 4 * g + r < qmin[kb] ||
@@ -961,11 +959,10 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
             if (out) x = -__builtin_huge_valf();
           }
           p[qb2][kb][r] = __builtin_amdgcn_exp2f(x);
-          ds[qb2][kb][r] = p[qb2][kb][r] * (dp[cur][qb2][kb][r] - dq[r]);
+          ds[qb2][kb][r] = p[qb2][kb][r] * (dp[qb2][kb][r] - dq[r]);
         }
       }
     }
-    if (LOC && qs + 1 < NS) scores(qs + 1, sc[cur ^ 1], dp[cur ^ 1]);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const float pv[8] = {p[0][kb][0], p[0][kb][1], p[0][kb][2], p[0][kb][3],
@@ -992,10 +989,11 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
   }
 }
 
-// NW waves of KB key blocks each cover the workgroup's 128 key rows; query
-// tiles of BQ rows.
+// NW waves of KB key blocks each cover the workgroup's 16 * NW * KB key
+// rows; query tiles of BQ rows. At most 168 VGPRs: 3 waves per SIMD.
 template <typename T, int D, bool GLOB, int NW, int KB, int BQ>
-__global__ __launch_bounds__(64 * NW) void dkdv2_kernel(BwdArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3)))
+void dkdv2_kernel(BwdArgs a) {
   using Tile = SwzTile<D, BQ>;
   constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = BQ;
   static_assert(BQ == 32 || BQ == 64 || BQ == 128, "query tile rows");
@@ -1262,10 +1260,11 @@ constexpr int kDkdvGlobWaves = 12;
 constexpr int kDkdvLocalWaves = 4;
 constexpr int kDkdvKB = 1;  // 16-key blocks per wave
 constexpr int kDqWaves = 4;
-// Query rows per dK/dV tile (with 8-wave local workgroups 32 and 128
-// measured 6% and 3% slower, equal on the global kernel).
+// Query rows per dK/dV tile. The local kernel's 32-row tiles keep its LDS
+// at 33 KB, so three 4-wave workgroups (3 waves per SIMD, 160 VGPRs) fit on
+// a CU; with 64-row tiles only two fit.
 constexpr int kDkdvGlobBQ = 64;
-constexpr int kDkdvLocalBQ = 64;
+constexpr int kDkdvLocalBQ = 32;
 
 template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
