@@ -638,20 +638,20 @@ __device__ __forceinline__ LaneOffs<D> lane_offs(int lane) {
   return o;
 }
 
-// Query-centric dQ for QB blocks of 16 queries per wave against one 64-key
-// tile: S = K . Q^T and dP = V . dO^T (key on rows), dS = P * (dP - Delta),
-// dQ^T += K^T . dS^T.
-template <typename T, int D, int QB, bool MASK>
+// Query-centric dQ for QB blocks of 16 queries per wave against one BN-key
+// tile, in 32-key halves: S = K . Q^T and dP = V . dO^T (key on rows),
+// dS = P * (dP - Delta), dQ^T += K^T . dS^T.
+template <typename T, int D, int QB, int BN, bool MASK>
 __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const LaneOffs<D>& lo,
                                          const Frag<T> (&qf)[QB][D / 32],
                                          const Frag<T> (&df)[QB][D / 32],
                                          f32x4 (&dqa)[D / 16][QB], const float (&lse2)[QB],
                                          const float (&dl)[QB], float c2, int g,
                                          const TileMask& mk, bool half0, bool half1) {
-  using Tile = SwzTile<D, 64>;
+  using Tile = SwzTile<D, BN>;
   constexpr int NC = D / 32;
 #pragma unroll
-  for (int kc = 0; kc < 2; ++kc) {
+  for (int kc = 0; kc < BN / 32; ++kc) {
     // masked tiles: a 32-key half with no key visible to the wave is skipped
     if (MASK && !(kc ? half1 : half0)) continue;
     float ds[2][QB][4];  // [h][qb][r]
@@ -713,14 +713,13 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
   }
 }
 
-// NW waves of QB blocks of 16 queries each cover the workgroup's 128
-// queries; at least 2 waves per SIMD.
-template <typename T, int D, int NW, int QB>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+// NW waves of QB blocks of 16 queries each cover the workgroup's
+// 16 * NW * QB queries; key tiles of BN rows; at least WPE waves per SIMD.
+template <typename T, int D, int NW, int QB, int BN, int WPE>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE)))
 void dq2_kernel(BwdArgs a) {
-  using Tile = SwzTile<D, 64>;
-  constexpr int kQW = 16 * QB, kBM = NW * kQW, kBN = 64;
-  static_assert(kBM == 128, "128 queries per workgroup");
+  using Tile = SwzTile<D, BN>;
+  constexpr int kQW = 16 * QB, kBM = NW * kQW, kBN = BN;
   // Two pipeline stages as separate LDS objects (see fwd2_kernel).
   __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];  // K, V
   __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
@@ -865,9 +864,9 @@ void dq2_kernel(BwdArgs a) {
       const int vis_hi = loc ? q_last - ts : wg_hi - 1 - ts;
       const bool half0 = vis_lo <= 31, half1 = vis_hi >= 32;
       if (full)
-        dq2_tile<T, D, QB, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, true, true);
+        dq2_tile<T, D, QB, BN, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, true, true);
       else
-        dq2_tile<T, D, QB, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, half0, half1);
+        dq2_tile<T, D, QB, BN, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, half0, half1);
     }
   };
   for (int it = 0; it < ntot; it += 2) {
@@ -1254,12 +1253,17 @@ void dkdv2_kernel(BwdArgs a) {
 // backward, 4 waves 3% slower than 8); the local
 // kernel 4 waves (64 rows: its band of queries, 64 + W - 1, wastes fewer
 // pairs than with 128 rows; measured 7% faster). dQ workgroups: 4 waves of
-// 32 queries (each K/V fragment read from LDS serves two query blocks; 8
-// waves of 16 queries measured 27% slower at D = 128).
+// 32 queries, 64-key tiles, 2 waves per SIMD at 249 VGPRs (each K/V
+// fragment read from LDS serves two query blocks). 16 queries per wave
+// lose that reuse: 8 waves measured 27% slower, and with 32-key tiles at
+// 3 or 4 waves per SIMD still 5-10% slower backward at D = 128.
 constexpr int kDkdvGlobWaves = 12;
 constexpr int kDkdvLocalWaves = 4;
 constexpr int kDkdvKB = 1;  // 16-key blocks per wave
 constexpr int kDqWaves = 4;
+constexpr int kDqQB = 2;    // 16-query blocks per dQ wave
+constexpr int kDqBN = 64;   // key rows per dQ tile
+constexpr int kDqWPE = 2;   // dQ waves per SIMD (register budget)
 // Query rows per dK/dV tile. The local kernel's 32-row tiles keep its LDS
 // at 33 KB, so three 4-wave workgroups (3 waves per SIMD, 160 VGPRs) fit on
 // a CU; with 64-row tiles only two fit.
@@ -1277,7 +1281,8 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   // work items per document: query tiles (dQ), global-row tiles x query
   // chunks (global dK/dV), key tiles (local dK/dV); all tiles are 128 rows
   BwdArgs aq = a, ag = a, al = a;
-  set_items(aq.docs, [&](int d) { return (a.docs.len[d] + Tr::kBM - 1) / Tr::kBM; });
+  constexpr int kQM = sizeof(T) == 2 ? 16 * kDqWaves * kDqQB : Tr::kBM;  // dQ queries per workgroup
+  set_items(aq.docs, [&](int d) { return (a.docs.len[d] + kQM - 1) / kQM; });
   constexpr bool kMfma = sizeof(T) == 2;
   constexpr int kGK = kMfma ? 16 * kDkdvGlobWaves * kDkdvKB : Tr::kBK;   // rows per workgroup
   constexpr int kLK = kMfma ? 16 * kDkdvLocalWaves * kDkdvKB : Tr::kBK;
@@ -1289,7 +1294,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   const int nq = aq.docs.item0[a.docs.n], ng = ag.docs.item0[a.docs.n];
   const int nl = al.docs.item0[a.docs.n];
   if constexpr (sizeof(T) == 2) {
-    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, 8 / kDqWaves>), dim3(nq * a.B * a.Hq),
+    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, kDqQB, kDqBN, kDqWPE>), dim3(nq * a.B * a.Hq),
                        dim3(64 * kDqWaves), 0, st, aq);
     hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvGlobWaves, kDkdvKB, kDkdvGlobBQ>),
                        dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvGlobWaves), 0, st, ag);
