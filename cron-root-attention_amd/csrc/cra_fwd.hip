@@ -410,11 +410,13 @@ __device__ __forceinline__ void attend_half(const char* tK, const char* tV, int 
 }
 
 // NW waves of 32 queries share each K/V tile of BN = 64 rows (2 x 32 KB
-// double buffer at D = 128); at least 2 waves per SIMD. PH selects the key
+// double buffer at D = 128); at least 2 waves per SIMD at D = 128 (240
+// VGPRs), 3 below it (168 VGPRs at D = 64, where the compiler's own choice
+// of 174 allowed only 2: the D = 64 forward is 8% faster at 3). PH selects the key
 // phases (bit 0 local window, bit 1 global rows) at compile time, so the
 // phase-restricted launches are kernels of their own in a trace.
 template <typename T, int D, int NW, int PH>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 3)))
 void fwd2_kernel(FwdArgs a) {
   constexpr int BN = 64;
   using Tile = SwzTile<D, BN>;
