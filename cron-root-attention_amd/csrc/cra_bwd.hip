@@ -886,7 +886,7 @@ void dq2_kernel(BwdArgs a) {
 
 // Key-centric dK/dV: each wave owns KB blocks of 16 key rows (rows of k/v,
 // or packed global rows with GLOB), B operands in registers; query tiles of
-// 64 rows of Q and dO stream through LDS with their LSE and Delta. A key row
+// BQ rows of Q and dO stream through LDS with their LSE and Delta. A key row
 // j sees the queries [j, j+W-1] (local) or [first_query(j), S) (global rows),
 // so every mask is a per-key interval.
 template <typename T, int D, int KB, int BQ, bool MASK, bool LOC>
@@ -1279,7 +1279,8 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq),
                        dim3(256), 0, st, a);
   // work items per document: query tiles (dQ), global-row tiles x query
-  // chunks (global dK/dV), key tiles (local dK/dV); all tiles are 128 rows
+  // chunks (global dK/dV), key tiles (local dK/dV), each of its kernel's
+  // workgroup size
   BwdArgs aq = a, ag = a, al = a;
   constexpr int kQM = sizeof(T) == 2 ? 16 * kDqWaves * kDqQB : Tr::kBM;  // dQ queries per workgroup
   set_items(aq.docs, [&](int d) { return (a.docs.len[d] + kQM - 1) / kQM; });
