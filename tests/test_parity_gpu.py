@@ -230,6 +230,9 @@ BWD_CASES = [
     (F16, 1, 2, 2, 100, 64, 2), (F16, 1, 2, 2, 2049, 128, 2), (F16, 1, 4, 2, 3000, 128, 2),
     (BF16, 1, 2, 2, 2500, 64, 2), (F32, 1, 2, 2, 1500, 32, 2), (F32, 1, 2, 2, 4096, 64, 3),
     (F16, 2, 2, 2, 700, 128, 2), (F16, 1, 2, 2, 2600, 80, 2), (F16, 1, 4, 1, 5000, 64, 2),
+    # 2-byte types at D = 32 (and 16, padded to 32): tiles whose fill takes
+    # fewer instructions than the kernels have waves
+    (F16, 1, 2, 2, 3000, 32, 2), (BF16, 1, 2, 2, 2100, 16, 2),
 ]
 
 
