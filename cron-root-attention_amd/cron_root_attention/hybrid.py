@@ -5,7 +5,7 @@ The reference's crossover (1536 tokens, hybrid.py:22) was measured on an RTX
 ``bench.py --crossover`` against ROCm's fused (flash) SDPA, causal, for
 forward and forward+backward separately: ``CROSSOVER_GFX950``.  Below a few
 thousand tokens the sqrt(N) op costs its launch floor (about 37 us forward,
-180 us forward+backward) while SDPA grows with B*H*S^2, so the crossover
+190-210 us forward+backward) while SDPA grows with B*H*S^2, so the crossover
 falls as B*H grows; the table keeps one row per measured B*H.
 ``_SDPA_THRESHOLD`` is the forward+backward crossover at D=128 for B*H=16,
 the role of the reference's constant.
@@ -27,9 +27,9 @@ from .core import cron_root_attention_v14
 # (1, 8, 64, fp16), (1, 12, 64, fp16).
 CROSSOVER_GFX950 = {
     ("fwd", 128, 1): 768,      # B=1 H=16 fp16 (fwd 0.037 vs 0.044 ms at S=768)
-    ("fwd", 128, 64): 512,     # B=2 H=32 bf16 (0.038 vs 0.041 ms at S=512)
-    ("train", 128, 1): 1024,   # B=1 H=16 fp16 (0.181 vs 0.199 ms at S=1024)
-    ("train", 128, 64): 512,   # B=2 H=32 bf16 (0.182 vs 0.191 ms at S=512)
+    ("fwd", 128, 64): 512,     # B=2 H=32 bf16 (0.040 vs 0.041 ms at S=512)
+    ("train", 128, 1): 1536,   # B=1 H=16 fp16 (0.194 vs 0.324 ms at S=1536; 0.204 vs 0.200 at 1024)
+    ("train", 128, 64): 768,   # B=2 H=32 bf16 (0.193 vs 0.312 ms at S=768)
     ("fwd", 64, 1): 1536,      # B=1 H=8 and H=12 fp16
     ("train", 64, 1): 2048,    # B=1 H=8 and H=12 fp16
 }
