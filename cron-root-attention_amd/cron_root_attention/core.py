@@ -124,6 +124,27 @@ def _check_inputs(q, k, v, kv_groups):
         raise ValueError("q, k, v must be on the same device")
 
 
+def _relay_scale(relay_log_scale, relay_on: bool, q: torch.Tensor, Hkv: int):
+    """exp(relay_log_scale) rounded to the input dtype (core.py:3541-3544), as
+    the fp32 [H_kv] multipliers the kernels read, or None.
+
+    The tensor must live on q's device: the kernels dereference its pointer
+    on the GPU, so a host tensor is rejected here, before any launch (the
+    reference fails the same call with a device-mismatch error in
+    ``relay_k * _relay_scale``).
+    """
+    if relay_log_scale is None or not relay_on:   # unused without relay (core.py:3541)
+        return None
+    if not isinstance(relay_log_scale, torch.Tensor):
+        raise TypeError("relay_log_scale must be a tensor of shape [H_kv]")
+    if relay_log_scale.device != q.device:
+        raise ValueError(f"relay_log_scale is on {relay_log_scale.device} but q is on "
+                         f"{q.device}; move it to the same device")
+    if relay_log_scale.shape != (Hkv,):
+        raise ValueError(f"relay_log_scale must have shape [{Hkv}]")
+    return relay_log_scale.detach().exp().to(q.dtype).to(torch.float32).contiguous()
+
+
 class CronRootAttentionV14Function(torch.autograd.Function):
     """Autograd of the three-phase attention (reference core.py:2822-3759).
 
@@ -151,12 +172,7 @@ class CronRootAttentionV14Function(torch.autograd.Function):
         qp, kp, vp = (_kernel_ready(_pad_d(t, Dp)) for t in (q, k, v))
         p = _native.problem(B, Hq, Hkv, S, Dp, W, relay_on, relay_top_k, q.dtype,
                             1.0 / math.sqrt(D))
-        rscale = None
-        if relay_log_scale is not None and relay_on:
-            if relay_log_scale.shape != (Hkv,):
-                raise ValueError(f"relay_log_scale must have shape [{Hkv}]")
-            # exp(alpha) rounded to the input dtype, as core.py:3542
-            rscale = relay_log_scale.detach().exp().to(q.dtype).to(torch.float32).contiguous()
+        rscale = _relay_scale(relay_log_scale, relay_on, q, Hkv)
         gk, gv, src = _native.build_global(p, kp, vp, rscale)
         o, lse = _native.forward(p, qp, kp, vp, gk, gv)
         ctx.problem = p
@@ -249,11 +265,7 @@ class CronRootAttentionVarlenFunction(torch.autograd.Function):
         qp, kp, vp = (_kernel_ready(_pad_d(t, Dp)) for t in (q, k, v))
         p = _native.problem(B, Hq, Hkv, S, Dp, 0, any_relay, relay_top_k, q.dtype,
                             1.0 / math.sqrt(D))
-        rscale = None
-        if relay_log_scale is not None and any_relay:
-            if relay_log_scale.shape != (Hkv,):
-                raise ValueError(f"relay_log_scale must have shape [{Hkv}]")
-            rscale = relay_log_scale.detach().exp().to(q.dtype).to(torch.float32).contiguous()
+        rscale = _relay_scale(relay_log_scale, any_relay, q, Hkv)
         gk, gv, src = _native.build_global_varlen(p, docs, kp, vp, rscale)
         o, lse = _native.forward_varlen(p, docs, qp, kp, vp, gk, gv)
         ctx.problem = p

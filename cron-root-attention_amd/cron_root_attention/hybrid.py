@@ -8,7 +8,10 @@ thousand tokens the sqrt(N) op costs its launch floor (about 37 us forward,
 190-210 us forward+backward) while SDPA grows with B*H*S^2, so the crossover
 falls as B*H grows; the table keeps one row per measured B*H.
 ``_SDPA_THRESHOLD`` is the forward+backward crossover at D=128 for B*H=16,
-the role of the reference's constant.
+the role of the reference's constant.  Both entry points default to
+``threshold=None``, which looks the crossover up in the table for the call's
+head dim, B*H and grad mode; an integer threshold behaves as the reference's
+(S >= threshold runs the sqrt(N) op).
 """
 from __future__ import annotations
 
@@ -47,9 +50,19 @@ def crossover(head_dim: int, training: bool, batch_heads: int = 1) -> int:
     return CROSSOVER_GFX950[(mode, d, bh)]
 
 
+def dispatch_backend(S: int, head_dim: int, training: bool, batch_heads: int = 1,
+                     threshold: Optional[int] = None) -> str:
+    """Backend the ``"auto"`` mode picks: ``"cron_root"`` when S >= threshold
+    (reference hybrid.py:58-64), else ``"sdpa"``; ``threshold=None`` uses the
+    measured gfx950 crossover (:func:`crossover`)."""
+    if threshold is None:
+        threshold = crossover(head_dim, training, batch_heads)
+    return "cron_root" if S >= threshold else "sdpa"
+
+
 def cron_root_attention_hybrid(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                backend: Literal["auto", "cron_root", "sdpa"] = "auto",
-                               threshold: Optional[int] = _SDPA_THRESHOLD) -> torch.Tensor:
+                               threshold: Optional[int] = None) -> torch.Tensor:
     """SDPA below ``threshold`` tokens, the sqrt(N) kernel at or above it
     (reference hybrid.py:25-64).  ``threshold=None`` picks the measured gfx950
     crossover for this head dim and for training vs inference (grad mode)."""
@@ -60,10 +73,9 @@ def cron_root_attention_hybrid(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
         return F.scaled_dot_product_attention(q, k, v, is_causal=True)
     if backend != "auto":
         raise ValueError(f"unknown backend {backend!r}")
-    if threshold is None:
-        threshold = crossover(q.shape[-1], torch.is_grad_enabled() and q.requires_grad,
-                              q.shape[0] * q.shape[1])
-    if S >= threshold:
+    training = torch.is_grad_enabled() and q.requires_grad
+    if dispatch_backend(S, q.shape[-1], training, q.shape[0] * q.shape[1],
+                        threshold) == "cron_root":
         return cron_root_attention_v14(q, k, v)
     return F.scaled_dot_product_attention(q, k, v, is_causal=True)
 
@@ -71,7 +83,7 @@ def cron_root_attention_hybrid(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
 class CronRootAttentionHybrid(nn.Module):
     """Projections + hybrid dispatch (reference hybrid.py:67-124)."""
 
-    def __init__(self, d_model: int, n_heads: int, threshold: int = _SDPA_THRESHOLD,
+    def __init__(self, d_model: int, n_heads: int, threshold: Optional[int] = None,
                  dropout: float = 0.0, bias: bool = False):
         super().__init__()
         self.d_model = d_model

@@ -17,7 +17,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .core import cron_root_attention_v14
-from .hybrid import crossover
+from .hybrid import dispatch_backend
 
 
 class CronRootAttention(nn.Module):
@@ -50,14 +50,15 @@ class CronRootAttention(nn.Module):
             if lin.bias is not None:
                 nn.init.zeros_(lin.bias)
 
-    def _use_sdpa(self, S: int, x: torch.Tensor) -> bool:
+    def backend_for(self, x: torch.Tensor) -> str:
+        """``"cron_root"`` or ``"sdpa"``: what forward(x) runs.  Without
+        ``hybrid`` always the sqrt(N) op; with it the crossover of
+        :func:`dispatch_backend` for this head dim, B*H and train/eval mode."""
         if not self.hybrid:
-            return False
-        thr = self.threshold
-        if thr is None:
-            thr = crossover(self.head_dim, self.training and torch.is_grad_enabled(),
-                            x.shape[0] * self.n_heads)
-        return S < thr
+            return "cron_root"
+        return dispatch_backend(x.shape[1], self.head_dim,
+                                self.training and torch.is_grad_enabled(),
+                                x.shape[0] * self.n_heads, self.threshold)
 
     def forward(self, x: torch.Tensor, kv: Optional[torch.Tensor] = None) -> torch.Tensor:
         B, S, _ = x.shape
@@ -65,7 +66,7 @@ class CronRootAttention(nn.Module):
         q = self.q_proj(x).view(B, S, self.n_heads, self.head_dim).transpose(1, 2)
         k = self.k_proj(kv).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(kv).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
-        if self._use_sdpa(S, x):
+        if self.backend_for(x) == "sdpa":
             out = F.scaled_dot_product_attention(q, k, v, is_causal=True,
                                                  enable_gqa=self.kv_groups > 1)
         else:
@@ -112,9 +113,11 @@ class CronRootMultiheadAttention(nn.Module):
                 key_padding_mask: Optional[torch.Tensor] = None, need_weights: bool = False,
                 attn_mask: Optional[torch.Tensor] = None, average_attn_weights: bool = True,
                 is_causal: bool = True) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-        if not self.batch_first:
-            query, key, value = (t.transpose(0, 1) for t in (query, key, value))
+        # self-attention only (reference module.py:223); checked before the
+        # batch_first transpose, which makes three distinct views of one tensor
         assert query is key and key is value, "Cross-attention not yet supported"
+        if not self.batch_first:
+            query = query.transpose(0, 1)
         B, S, E = query.shape
         qkv = F.linear(query, self.in_proj_weight, self.in_proj_bias)
         qkv = qkv.view(B, S, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)

@@ -10,7 +10,8 @@
 // (the reference streams every relay row for every tile).
 // Scores are fp32 dot(q, k) * scale; P is rounded to the input dtype before
 // P.V (core.py:1027, 1086, 1141); O = acc / l and LSE = m + ln(l)
-// (core.py:1147-1158).
+// (core.py:1147-1158). Unlike the reference, whose l sums the unrounded P
+// (core.py:1028), l sums the rounded P of the 2-byte types.
 //
 // Mapping: one workgroup = 4 waves = 128 consecutive queries of one (b, h);
 // each wave owns 32 queries. K/V tiles of 64 rows (32 for fp32) are staged in
@@ -248,8 +249,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
 // K/V tiles (64 rows) are double-buffered in swizzled LDS, filled with
 // global_load_lds while the previous tile is computed, V^T operands come from
 // ds_read_b64_tr_b16 on the row-major V tile, each tile is processed in two
-// 32-key halves, and the running max is raised only when a score exceeds it
-// by more than 2^8 (P stays <= 256; O and LSE are exact for any reference max).
+// 32-key halves, and the running max is raised only when the rounded
+// exponentials of a half against it sum past 2^15 (each P stays <= 2^15;
+// O and LSE are exact for any reference max). The normaliser l sums the
+// rounded P that the P.V MFMAs use.
 // ---------------------------------------------------------------------------
 template <int D>
 struct Fwd2Lane {
@@ -307,10 +310,12 @@ __device__ __forceinline__ void pv_half(const char* tV, int kh, const Fwd2Lane<D
 constexpr float kSumMax = 32768.f;
 
 // Exponentials of one 32-key half (8 per lane and query block) against the
-// running maximum, and their sum.
-template <bool MASK>
+// running maximum, rounded to the input type, and the sum of the rounded
+// values (the P.V operand and its normaliser).
+template <typename T, bool MASK>
 __device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float c2, float m,
-                                         int g, const TileMask& mk, float (&pv)[8], float& ps) {
+                                         int g, const TileMask& mk, Frag<T>& pk, float& ps) {
+  float pv[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -318,17 +323,19 @@ __device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float
       if (MASK && !mk.ok(32 * kc + 16 * h + 4 * g + r, qb)) s[h][qb][r] = -__builtin_huge_valf();
       pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -m));
     }
-  ps = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+  pk = pack8<T>(pv);
+  ps = frag_sum(pk);
 }
 
 // Raise the running maximum of query block qb to this half's maximum,
 // rescale its accumulators and redo the half's exponentials. Taken for the
 // first visible keys and whenever a score exceeds the running maximum by
-// enough to push a sum of 8 terms past kSumMax (NaN sums included).
-template <int D>
+// enough to push a sum of 8 rounded terms past kSumMax (inf and NaN sums
+// included).
+template <typename T, int D>
 __device__ __forceinline__ void half_rescale(f32x4 (&s)[2][2], int qb, float c2,
                                              f32x4 (&acc)[D / 16][2], float (&m_run)[2],
-                                             float (&l_run)[2], float (&pv)[8], float& ps) {
+                                             float (&l_run)[2], Frag<T>& pk, float& ps) {
   float mx = -__builtin_huge_valf();
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -342,11 +349,13 @@ __device__ __forceinline__ void half_rescale(f32x4 (&s)[2][2], int qb, float c2,
   for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
   m_run[qb] = m_new;
   const float mu = m_new == -__builtin_huge_valf() ? 0.f : m_new;
+  float pv[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int r = 0; r < 4; ++r) pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -mu));
-  ps = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+  pk = pack8<T>(pv);
+  ps = frag_sum(pk);
 }
 
 // One BN-key tile for the wave's 32 queries, in 32-key halves. The online
@@ -368,18 +377,19 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
   Frag<T> pf[2];
 #pragma unroll
   for (int kc = 0; kc < kHalves; ++kc) {
-    float pv[2][8], ps[2];
+    Frag<T> pn[2];
+    float ps[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
-      half_exp<MASK>(s[kc], kc, qb, c2, m_run[qb], g, mk, pv[qb], ps[qb]);
+      half_exp<T, MASK>(s[kc], kc, qb, c2, m_run[qb], g, mk, pn[qb], ps[qb]);
     if (kc > 0) pv_half<T, D, BN>(tV, kc - 1, lo, pf, acc);  // beside this half's exponentials
     if (kc + 1 < kHalves) tile_scores<T, D, BN>(tK, lo, qf, kc + 1, s[kc + 1]);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       if (__any(!(ps[qb] <= kSumMax)))
-        half_rescale<D>(s[kc], qb, c2, acc, m_run, l_run, pv[qb], ps[qb]);
+        half_rescale<T, D>(s[kc], qb, c2, acc, m_run, l_run, pn[qb], ps[qb]);
       l_run[qb] += ps[qb];
-      pf[qb] = pack8<T>(pv[qb]);
+      pf[qb] = pn[qb];
     }
   }
   pv_half<T, D, BN>(tV, kHalves - 1, lo, pf, acc);
@@ -396,15 +406,14 @@ __device__ __forceinline__ void attend_half(const char* tK, const char* tV, int 
   using Tile = SwzTile<D, BN>;
   f32x4 s[2][2];
   tile_scores<T, D, BN>(tK, lo, qf, kc, s);
-  float pv[2][8], ps[2];
+  float ps[2];
   Frag<T> pf[2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) half_exp<true>(s, kc, qb, c2, m_run[qb], g, mk, pv[qb], ps[qb]);
+  for (int qb = 0; qb < 2; ++qb) half_exp<T, true>(s, kc, qb, c2, m_run[qb], g, mk, pf[qb], ps[qb]);
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    if (__any(!(ps[qb] <= kSumMax))) half_rescale<D>(s, qb, c2, acc, m_run, l_run, pv[qb], ps[qb]);
+    if (__any(!(ps[qb] <= kSumMax))) half_rescale<T, D>(s, qb, c2, acc, m_run, l_run, pf[qb], ps[qb]);
     l_run[qb] += ps[qb];
-    pf[qb] = pack8<T>(pv[qb]);
   }
   pv_half<T, D, BN>(tV, kc, lo, pf, acc);
 }

@@ -355,6 +355,84 @@ def forward_backward(q, k, v, dO, plan: Plan, kv_groups: int = 1,
 
 
 # ---------------------------------------------------------------------------
+# Gradients of chosen rows (spot checks at sizes where full autograd is slow)
+# ---------------------------------------------------------------------------
+
+def query_row_grads(q, k, v, dO, plan: Plan, rows: tuple, kv_groups: int = 1,
+                    src: Optional[torch.Tensor] = None):
+    """dQ of queries [lo, hi) by fp64 autograd of :func:`forward` restricted to
+    those rows.  O_i depends on q only through q_i, so differentiating the
+    restricted forward with dO[lo:hi] gives exactly rows [lo, hi) of the full
+    dQ (the reference's K4, core.py:1165-1316).  Returns [B, Hq, hi-lo, D]."""
+    lo, hi = rows
+    q64 = q.detach().to(torch.float64).requires_grad_(True)
+    o, _, _ = forward(q64, k, v, plan, kv_groups, src=src, rows=rows)
+    o.backward(dO[:, :, lo:hi].to(torch.float64))
+    return q64.grad[:, :, lo:hi].detach()
+
+
+def key_multiplicity(j: int, plan: Plan, src_row) -> np.ndarray:
+    """How many times key row j occurs in the multiset of every query
+    (int64 [S]): once for the queries whose local window holds it
+    (i in [j, j+W-1], core.py:1016-1017), once more if j = s*W is a strided
+    row and ls(i) > j (core.py:1060-1061), and once per relay token t with
+    src[t] = j and (t//top_k + 1)*W - 1 < ls(i) (core.py:1115-1117).
+    ``src_row``: the relay source rows of this (b, kv head), [NB*top_k]."""
+    S, W = plan.S, plan.W
+    i = np.arange(S, dtype=np.int64)
+    ls = np.maximum(i - W + 1, 0)
+    m = ((i >= j) & (i <= j + W - 1)).astype(np.int64)
+    if j % W == 0:
+        m += (ls > j)
+    if plan.relay:
+        for t in np.nonzero(np.asarray(src_row) == j)[0]:
+            r = int(t) // plan.top_k
+            m += (ls > (r + 1) * W - 1)
+    return m
+
+
+def key_row_grads(q, k, v, dO, plan: Plan, keys, lse, delta, src=None, kv_groups: int = 1):
+    """dK and dV of the chosen key rows in closed form, fp64.
+
+    For key row j of kv head g, summed over the query heads h of the group
+    and over every query i that sees j (with the multiplicity of
+    :func:`key_multiplicity`):
+      P_ij = exp(q_i.k_j * scale - lse_i)
+      dV_j = sum m_ij P_ij dO_i
+      dK_j = scale * sum m_ij P_ij (dO_i.v_j - delta_i) q_i
+    with delta_i = O_i.dO_i (the backward of core.py:1165-1316, 1650-1745,
+    1755-1889, 2381-2492 plus the relay scatter, core.py:2767-2815, all
+    landing on the source row).  ``lse`` and ``delta`` ([B, Hq, S]) must come
+    from the exact forward.  No relay scale.  ``keys``: iterable of
+    (b, g, j).  Returns {(b, g, j): (dK_j, dV_j)} as fp64 [D] tensors.
+    """
+    W = plan.W
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D)
+    if plan.relay and src is None:
+        src = relay_select(k, plan)
+    out = {}
+    for (b, g, j) in keys:
+        src_row = src[b, g].numpy() if plan.relay else None
+        m = key_multiplicity(j, plan, src_row)
+        idx = torch.from_numpy(np.nonzero(m)[0])
+        mm = torch.from_numpy(m[idx.numpy()]).to(torch.float64)
+        kj = k[b, g, j].to(torch.float64)
+        vj = v[b, g, j].to(torch.float64)
+        dk = torch.zeros(D, dtype=torch.float64)
+        dv = torch.zeros(D, dtype=torch.float64)
+        for h in range(g * kv_groups, (g + 1) * kv_groups):
+            qi = q[b, h, idx].to(torch.float64)
+            doi = dO[b, h, idx].to(torch.float64)
+            p = torch.exp(qi @ kj * scale - lse[b, h, idx].to(torch.float64)) * mm
+            dv += p @ doi
+            ds = p * (doi @ vj - delta[b, h, idx].to(torch.float64))
+            dk += scale * (ds @ qi)
+        out[(b, g, j)] = (dk, dv)
+    return out
+
+
+# ---------------------------------------------------------------------------
 # Packed documents (varlen, core.py:3836-3954)
 # ---------------------------------------------------------------------------
 

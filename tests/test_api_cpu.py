@@ -107,3 +107,32 @@ def test_crossover_table_lookup():
         for d in (64, 128):
             seq = [crossover(d, mode == "train", bh) for bh in (1, 16, 64, 1024)]
             assert seq == sorted(seq, reverse=True)
+
+
+def test_hybrid_defaults_use_the_measured_table():
+    import inspect
+    from cron_root_attention.hybrid import crossover, dispatch_backend
+    assert inspect.signature(cra.cron_root_attention_hybrid).parameters["threshold"].default is None
+    assert cra.CronRootAttentionHybrid(64, 2).threshold is None
+    # config 5 (B*H = 64, D = 128): the gfx950 training crossover, not the static 1536
+    thr = crossover(128, True, 64)
+    assert thr < 1536
+    assert dispatch_backend(thr - 1, 128, True, 64) == "sdpa"
+    assert dispatch_backend(thr, 128, True, 64) == "cron_root"
+    assert dispatch_backend(1024, 128, True, 64, threshold=1536) == "sdpa"
+    assert dispatch_backend(1536, 128, True, 64, threshold=1536) == "cron_root"
+    m = cra.CronRootAttention(d_model=64, n_heads=2, hybrid=True, threshold=128)
+    assert m.backend_for(torch.zeros(1, 127, 64)) == "sdpa"
+    assert m.backend_for(torch.zeros(1, 128, 64)) == "cron_root"
+    assert cra.CronRootAttention(64, 2).backend_for(torch.zeros(1, 8, 64)) == "cron_root"
+
+
+def test_multihead_attention_self_attention_only_both_layouts():
+    m = cra.CronRootMultiheadAttention(64, 2, batch_first=False)
+    x = torch.randn(16, 1, 64)
+    with pytest.raises(AssertionError):
+        m(x, x.clone(), x)
+    # the same tensor passes the self-attention check in (S, B, E) layout and
+    # reaches the op, which refuses CPU tensors
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
+        m(x, x, x)

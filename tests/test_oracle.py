@@ -405,3 +405,80 @@ def test_varlen_relay_scale_gradient_sums_documents():
         e[h] = eps
         fd = (L(alpha + e) - L(alpha - e)) / (2 * eps)
         assert abs(fd - float(g["dalpha"][h])) < 1e-6
+
+
+# ------------------------------------------------ gradients of chosen rows
+
+def _grad_case(S, Hq, Hkv, D, seed, top_k=2):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, Hq, S, D, generator=g, dtype=torch.float64)
+    k = torch.randn(1, Hkv, S, D, generator=g, dtype=torch.float64)
+    v = torch.randn(1, Hkv, S, D, generator=g, dtype=torch.float64)
+    do = torch.randn(1, Hq, S, D, generator=g, dtype=torch.float64)
+    plan = O.Plan(S, O.window_size(S), True, top_k)
+    return q, k, v, do, plan
+
+
+def _strided_and_relay_keys(plan, src_row):
+    """Every key class: local-only, strided, relay source, and both."""
+    W = plan.W
+    src = set(int(x) for x in src_row)
+    strided = [r * W for r in range(plan.num_blocks)]
+    both = [j for j in strided if j in src]
+    relay_only = [j for j in sorted(src) if j % W]
+    local_only = [j for j in range(plan.S) if j % W and j not in src][:5]
+    return local_only + strided[:3] + strided[-2:] + relay_only[:6] + both
+
+
+def test_query_row_grads_equal_full_autograd():
+    q, k, v, do, plan = _grad_case(700, 4, 2, 32, seed=3)
+    _, _, _, g = O.forward_backward(q, k, v, do, plan, kv_groups=2)
+    for lo, hi in ((0, 40), (300, 333), (650, 700)):
+        dq = O.query_row_grads(q, k, v, do, plan, (lo, hi), kv_groups=2)
+        assert torch.allclose(dq, g["dq"][:, :, lo:hi], rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("kv_groups", [1, 2])
+def test_key_row_grads_equal_full_autograd(kv_groups):
+    S, Hkv, D = 900, 2, 32
+    q, k, v, do, plan = _grad_case(S, Hkv * kv_groups, Hkv, D, seed=5 + kv_groups)
+    # make block 7's strided row its top relay row (a key counted twice)
+    k[0, 1, 7 * plan.W] *= 4.0
+    o, lse, src, g = O.forward_backward(q, k, v, do, plan, kv_groups=kv_groups)
+    delta = (o * do).sum(-1)
+    assert int(src[0, 1, 7 * plan.top_k]) == 7 * plan.W
+    keys = [(0, h, j) for h in range(Hkv) for j in _strided_and_relay_keys(plan, src[0, h])]
+    res = O.key_row_grads(q, k, v, do, plan, keys, lse, delta, src, kv_groups)
+    for (b, h, j), (dk, dv) in res.items():
+        assert torch.allclose(dk, g["dk"][b, h, j], rtol=1e-9, atol=1e-11), (h, j)
+        assert torch.allclose(dv, g["dv"][b, h, j], rtol=1e-9, atol=1e-11), (h, j)
+
+
+@pytest.mark.parametrize("mutation", ["no_strided", "no_relay", "window_off_by_one"])
+def test_key_row_grads_catch_planted_mistakes(mutation, monkeypatch):
+    """A multiplicity that drops a term or shifts the window must disagree
+    with autograd on some key row."""
+    S, D = 900, 32
+    q, k, v, do, plan = _grad_case(S, 1, 1, D, seed=11)
+    k[0, 0, 4 * plan.W] *= 4.0
+    o, lse, src, g = O.forward_backward(q, k, v, do, plan)
+    delta = (o * do).sum(-1)
+    keys = [(0, 0, j) for j in _strided_and_relay_keys(plan, src[0, 0])]
+    true_mult = O.key_multiplicity
+
+    def wrong(j, pl, src_row):
+        if mutation == "no_strided":
+            m = true_mult(j, pl, src_row)
+            if j % pl.W == 0:
+                i = np.arange(pl.S)
+                m = m - (np.maximum(i - pl.W + 1, 0) > j)
+            return m
+        if mutation == "no_relay":
+            return true_mult(j, O.Plan(pl.S, pl.W, False, pl.top_k), None)
+        return true_mult(j, O.Plan(pl.S, pl.W + 1, pl.relay, pl.top_k), src_row)
+
+    monkeypatch.setattr(O, "key_multiplicity", wrong)
+    res = O.key_row_grads(q, k, v, do, plan, keys, lse, delta, src)
+    bad = sum(not torch.allclose(dk, g["dk"][b, h, j], rtol=1e-6, atol=1e-9)
+              for (b, h, j), (dk, dv) in res.items())
+    assert bad > 0
