@@ -103,6 +103,10 @@ _SIGNATURES = {
                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                ctypes.c_void_p, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
                                ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "cra_bwd_noalloc": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, CraTensor, CraTensor,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_void_p, ctypes.c_void_p, CraTensor, CraTensor,
+                                       CraTensor, ctypes.c_void_p, ctypes.c_void_p]),
     "cra_varlen_sizes": (ctypes.c_int, [_P, _D, ctypes.POINTER(ctypes.c_int64),
                                         ctypes.POINTER(ctypes.c_int64)]),
     "cra_build_global_varlen": (ctypes.c_int, [_P, _D, CraTensor, CraTensor, ctypes.c_void_p,
@@ -264,6 +268,32 @@ def backward(p: CraProblem, q, k, v, o, do, lse, gk, gv, src, relay_scale, want_
                        tensor_arg(dq), tensor_arg(dk), tensor_arg(dv),
                        dalpha.data_ptr() if dalpha is not None else None, ws.data_ptr(),
                        ws.numel(), _stream(q)), "cra_bwd")
+    return dq, dk, dv, dalpha
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20   # CRA_NOALLOC_SCRATCH_BYTES
+
+
+def backward_noalloc(p: CraProblem, q, k, v, o, do, lse, gk, gv, src, relay_scale,
+                     want_dalpha: bool, out=None):
+    """cra_bwd_noalloc: the backward without a workspace (the library's fixed
+    per-device scratch). ``out`` = (dq, dk, dv) preallocated outputs, else
+    they are allocated here."""
+    lib = load_library()
+    if out is None:
+        out = (torch.empty(q.shape, dtype=q.dtype, device=q.device),
+               torch.empty(k.shape, dtype=k.dtype, device=k.device),
+               torch.empty(v.shape, dtype=v.dtype, device=v.device))
+    dq, dk, dv = out
+    dalpha = (torch.empty(p.H_kv, dtype=torch.float32, device=q.device)
+              if (want_dalpha and p.relay) else None)
+    rs = relay_scale.data_ptr() if (relay_scale is not None and p.relay) else None
+    _check(lib.cra_bwd_noalloc(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                               tensor_arg(o), tensor_arg(do), lse.data_ptr(), gk.data_ptr(),
+                               gv.data_ptr(), src.data_ptr() if src is not None else None, rs,
+                               tensor_arg(dq), tensor_arg(dk), tensor_arg(dv),
+                               dalpha.data_ptr() if dalpha is not None else None, _stream(q)),
+           "cra_bwd_noalloc")
     return dq, dk, dv, dalpha
 
 

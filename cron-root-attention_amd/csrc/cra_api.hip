@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 #include "../../include/cra.h"
@@ -262,11 +263,14 @@ int fwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, c
   return CRA_OK;
 }
 
+// nchunk_cap > 0 limits the query chunks of the global-row partials (the
+// allocation-free entry point fits them into its fixed scratch); 0 keeps
+// the planned count.
 int bwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, cra_tensor v,
              cra_tensor o, cra_tensor dout, const float* lse, const void* glob_k,
              const void* glob_v, const int32_t* relay_src, const float* relay_scale,
              cra_tensor dq, cra_tensor dk, cra_tensor dv, float* dalpha, void* workspace,
-             size_t workspace_bytes_given, void* stream) {
+             size_t workspace_bytes_given, void* stream, int nchunk_cap = 0) {
   const int esz = elem_size(p->dtype);
   if (int e = check_tensor("q", q, esz)) return e;
   if (int e = check_tensor("k", k, esz)) return e;
@@ -286,7 +290,11 @@ int bwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, c
   if (int e = check_buf("glob_v", glob_v)) return e;
   if (pl.any_relay && !relay_src) return fail(CRA_E_INVALID, "relay_src is NULL with relay on");
   int nchunk = 0;
-  const size_t need = workspace_bytes(p, pl, &nchunk);
+  size_t need = workspace_bytes(p, pl, &nchunk);
+  if (nchunk_cap > 0 && nchunk > nchunk_cap) {
+    nchunk = nchunk_cap;
+    need = cra::bwd_workspace_layout(p->D, p->B, p->H_q, p->H_kv, p->S, pl.G, nchunk);
+  }
   if (need > 0 && (!workspace || workspace_bytes_given < need))
     return fail(CRA_E_WORKSPACE, "workspace of %zu bytes needed, %zu given", need,
                 workspace ? workspace_bytes_given : (size_t)0);
@@ -322,6 +330,46 @@ int bwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, c
     hipError_t e = cra::launch_bwd(p->dtype, p->D, a, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "cra_bwd launch");
   }
+  return CRA_OK;
+}
+
+// ---- allocation-free backward ----------------------------------------------
+// The workspace of cra_bwd_noalloc: one file-scope array per device, held
+// until the process ends. In host code `scratch` is only a handle; its
+// device address (different on every device) comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+static __device__ __align__(256) char scratch[CRA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, which must also be the
+// stream's device (the kernels run on the stream's device).
+int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+    if (sdev != dev)
+      return fail(CRA_E_INVALID,
+                  "stream belongs to device %d but device %d is current; make the stream's "
+                  "device current", (int)sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(CRA_E_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(CRA_E_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
   return CRA_OK;
 }
 
@@ -374,6 +422,32 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
   if (int e = plan_plain(p, &pl)) return e;
   return bwd_impl(p, pl, q, k, v, o, dout, lse, glob_k, glob_v, relay_src, relay_scale, dq, dk,
                   dv, dalpha, workspace, workspace_bytes, stream);
+}
+
+int cra_bwd_noalloc(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+                    cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
+                    const int32_t* relay_src, const float* relay_scale, cra_tensor dq,
+                    cra_tensor dk, cra_tensor dv, float* dalpha, void* stream) {
+  Plan pl;
+  if (int e = plan_plain(p, &pl)) return e;
+  int nchunk = 0;
+  const size_t planned = workspace_bytes(p, pl, &nchunk);
+  int cap = 0;  // keep the planned chunks if they fit: then results equal cra_bwd's bit for bit
+  if (planned > (size_t)CRA_NOALLOC_SCRATCH_BYTES) {
+    const size_t one = cra::bwd_workspace_layout(p->D, p->B, p->H_q, p->H_kv, p->S, pl.G, 1);
+    const size_t per_chunk = one - cra::bwd_workspace_layout(p->D, p->B, p->H_q, p->H_kv, p->S,
+                                                             pl.G, 0);
+    if (one > (size_t)CRA_NOALLOC_SCRATCH_BYTES)
+      return fail(CRA_E_WORKSPACE,
+                  "cra_bwd_noalloc: this problem needs %zu bytes of workspace even with one "
+                  "query chunk; the fixed scratch holds %u bytes (use cra_bwd with a "
+                  "caller-allocated workspace)", one, (unsigned)CRA_NOALLOC_SCRATCH_BYTES);
+    cap = (int)(((size_t)CRA_NOALLOC_SCRATCH_BYTES - (one - per_chunk)) / per_chunk);
+  }
+  void* ws = nullptr;
+  if (int e = scratch_address(stream, &ws)) return e;
+  return bwd_impl(p, pl, q, k, v, o, dout, lse, glob_k, glob_v, relay_src, relay_scale, dq, dk,
+                  dv, dalpha, ws, (size_t)CRA_NOALLOC_SCRATCH_BYTES, stream, cap);
 }
 
 int cra_varlen_sizes(const cra_problem* p, const cra_docs* docs, int64_t* global_rows,

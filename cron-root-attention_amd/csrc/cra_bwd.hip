@@ -1357,8 +1357,12 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
   if (nc > max_nc) nc = max_nc;
   if (nc < 1) nc = 1;
   *nchunk = (int)nc;
+  return bwd_workspace_layout(D, B, Hq, Hkv, S, G, (int)nc);
+}
+
+size_t bwd_workspace_layout(int D, int B, int Hq, int Hkv, int S, int64_t G, int nchunk) {
   const size_t delta = (((size_t)B * Hq * S * 4) + 255) / 256 * 256;
-  const size_t part = (size_t)nc * B * Hkv * G * 2 * D * 4;
+  const size_t part = (size_t)nchunk * B * Hkv * G * 2 * D * 4;
   return delta + part;
 }
 

@@ -11,13 +11,15 @@
  *  - Return value: 0 on success, a negative CRA_E_* code otherwise; the
  *    message of the last failure on the calling thread is available from
  *    cra_last_error(). No exceptions cross the ABI, no host synchronisation
- *    happens, nothing is allocated: the caller passes every buffer.
+ *    happens, nothing is allocated: the caller passes every buffer (the one
+ *    exception, cra_bwd_noalloc, uses a fixed device array of the library).
  *  - Tensors of shape [B, H, S, D] are passed as cra_tensor: a device pointer
  *    and element strides for B, H and S; D must be contiguous (stride 1), the
  *    pointer and every row start must be 16-byte aligned.
  *  - `stream` is a hipStream_t (0 = the null stream); all work is enqueued on it.
  *  - Concurrent calls on different streams are safe; the library keeps no
- *    mutable global state.
+ *    mutable global state (except the scratch of cra_bwd_noalloc, whose
+ *    concurrent calls on one device race).
  */
 #ifndef CRA_H_
 #define CRA_H_
@@ -133,6 +135,30 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
             cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
             const int32_t* relay_src, const float* relay_scale, cra_tensor dq, cra_tensor dk,
             cra_tensor dv, float* dalpha, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Size of the fixed device scratch of cra_bwd_noalloc, per device. */
+#define CRA_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* cra_bwd without a workspace argument and without any allocation: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference.
+ * The workspace is a file-scope device array of CRA_NOALLOC_SCRATCH_BYTES
+ * (64 MiB) that every device the library runs on holds until the process
+ * ends; its address is looked up once per device on the first call there.
+ * The stream must belong to the current device (else CRA_E_INVALID). The
+ * global-row partials keep cra_bwd's query-chunk count when it fits (the
+ * results are then bit-identical to cra_bwd's) and use fewer chunks
+ * otherwise (same gradients up to the fp32 summation order); a problem
+ * whose workspace exceeds the scratch even with one chunk returns
+ * CRA_E_WORKSPACE. Nothing in the scratch needs clearing: every call writes
+ * what it reads. All calls on one device share that device's scratch, so
+ * calls that overlap on one device (two streams, two threads) race: the
+ * caller must order them. Other arguments and results as cra_bwd. */
+int cra_bwd_noalloc(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+                    cra_tensor dout, const float* lse, const void* glob_k, const void* glob_v,
+                    const int32_t* relay_src, const float* relay_scale, cra_tensor dq,
+                    cra_tensor dk, cra_tensor dv, float* dalpha, void* stream);
 
 /* Documents packed along S (varlen): document d is rows
  * cu_seqlens[d] .. cu_seqlens[d+1]-1 of every [B, H, S, D] tensor and is

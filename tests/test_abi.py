@@ -218,3 +218,19 @@ def test_varlen_entry_points_validate_before_launch():
     rc = lib.cra_bwd_varlen(ctypes.byref(p), d, t, t, t, t, t, 0x10000, 0x10000, 0x10000,
                             0x10000, None, t, t, t, None, 0x10000, need - 1, None)
     assert rc == N.E_WORKSPACE
+
+
+def test_bwd_noalloc_rejects_problems_beyond_its_scratch():
+    """cra_bwd_noalloc refuses, before touching a device, a problem whose
+    workspace exceeds the fixed scratch even with one query chunk (here Delta
+    alone is 1 GiB), and validates the problem like cra_bwd."""
+    lib = N.load_library()
+    t = N.CraTensor(0x10000, 1 << 26, 1 << 19, 128)
+    big = prob(B=8, H_q=64, H_kv=64, S=524288, W=725)
+    rc = lib.cra_bwd_noalloc(ctypes.byref(big), t, t, t, t, t, 0x10000, 0x10000, 0x10000, 0x10000,
+                             None, t, t, t, None, None)
+    assert rc == N.E_WORKSPACE
+    assert "scratch" in lib.cra_last_error().decode()
+    rc = lib.cra_bwd_noalloc(ctypes.byref(prob(top_k=9)), t, t, t, t, t, 0x10000, 0x10000,
+                             0x10000, 0x10000, None, t, t, t, None, None)
+    assert rc == N.E_INVALID
