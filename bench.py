@@ -12,11 +12,19 @@ Prints ONE JSON line:
                with HIP events on the stream it runs on, against the fp16
                dense MFMA peak; traffic from a committed rocprofv3 --pmc
                summary when present
-  cpu_baseline the oracle's chunked CPU port on the host cores, on a bounded
-               sample of query rows of the same workload, as TFLOP/s
+  cpu_baseline the oracle's chunked CPU port (the reference's cra_cpu_fast
+               algorithm, fp32) on the host cores, on a bounded sample of whole
+               heads of the same workload, as TFLOP/s, with the CPU model and
+               the thread count used
 
-``--crossover`` instead sweeps S against torch's SDPA (forward and fwd+bwd)
-and prints one JSON line per point.
+Other modes:
+  --config N|all       time BASELINE configurations 2-5 at every listed S (ms,
+                       TFLOP/s, roofline fraction, 50% target; config 5 through
+                       the hybrid dispatcher with SDPA beside it), one JSON line
+                       per point
+  --crossover          sweep S against torch's SDPA (forward and fwd+bwd)
+  --profile-workload   short fixed workload for rocprofv3 --pmc passes
+  --counter-summary D  markdown summary of rocprofv3 --pmc output directories
 """
 from __future__ import annotations
 
@@ -124,10 +132,51 @@ def per_launch_ms(fn, steps, warmup, torch):
     return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
 
 
+def host_cpu() -> dict:
+    """CPU model, logical CPUs of the machine, CPUs this process may run on,
+    physical cores (from /proc/cpuinfo where readable)."""
+    model, phys = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            pid = core = None
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    pid = v
+                elif k == "core id":
+                    core = v
+                    phys.add((pid, core))
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count()
+    return {"cpu_model": model, "logical_cpus": os.cpu_count(), "cpus_allowed": allowed,
+            "physical_cores": len(phys) or None}
+
+
+def cpu_threads(requested=None) -> int:
+    """Threads for the CPU baseline: as requested, else the job's CPU share
+    (OMP_NUM_THREADS, which the GPU box sets to its share of the host), else
+    every CPU this process may run on."""
+    if requested:
+        return int(requested)
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return host_cpu()["cpus_allowed"] or 1
+
+
 def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
-    """Oracle CPU port (fp32 forward) on the host cores: pairs of heads of the
-    same workload, each over all S queries, until ~budget_s of CPU time (or
-    all H heads); returns effective TFLOP/s over the rows done."""
+    """Oracle CPU port (fp32 forward, the reference's cra_cpu_fast algorithm)
+    on the host cores: pairs of heads of the same workload, each over all S
+    queries, until ~budget_s of CPU time (or all H heads); the relay
+    selection (fp32 norms + topk, as cra_cpu_fast) is inside the timed
+    region. Returns effective TFLOP/s over the heads done."""
     import torch
     from oracle import cra_oracle as O
     from oracle.cpu_port import cra_cpu_chunked
@@ -138,16 +187,17 @@ def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
     g = torch.Generator().manual_seed(0)
     while heads_done < H and t_used < budget_s:
         q, k, v = (torch.randn(1, Hs, S, D, generator=g) for _ in range(3))
-        src = O.relay_select(k, plan, "lanetree")
         t0 = time.perf_counter()
-        cra_cpu_chunked(q, k, v, plan, src=src)
+        cra_cpu_chunked(q, k, v, plan, norm="torch")
         t_used += time.perf_counter() - t0
         heads_done += Hs
         flops += 4 * D * pairs_fast(S) * Hs
-    return {"value": flops / t_used / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"fp32 forward of {heads_done} of {H} heads (all {S} queries each), "
-                      f"D={D}, {t_used:.1f} s",
-            "seconds": round(t_used, 2)}
+    out = {"value": flops / t_used / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": f"fp32 forward of {heads_done} of {H} heads (all {S} queries each, relay "
+                     f"selection included), D={D}, {t_used:.1f} s on {threads} threads",
+           "seconds": round(t_used, 2)}
+    out.update(host_cpu())
+    return out
 
 
 def traffic_for(kernel: str, workload: str):
@@ -249,7 +299,7 @@ def run_main(args):
 
     cpu = None
     if not args.skip_cpu:
-        cpu = cpu_baseline(B, H, S, D, args.cpu_seconds, args.cpu_threads)
+        cpu = cpu_baseline(B, H, S, D, args.cpu_seconds, cpu_threads(args.cpu_threads))
 
     out = {
         "metric": METRIC, "value": round(f_all / (step_ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
@@ -267,11 +317,102 @@ def run_main(args):
     print(json.dumps(out), flush=True)
 
 
+# BASELINE configurations 2-5 (config 1 is the CPU reference's plumbing case):
+# (B, H, D, dtype, S values, mode). mode "fwd": forward under no_grad;
+# "train": forward + backward; "hybrid": CronRootAttention(hybrid=True)'s
+# dispatch (cron_root_attention_hybrid) in both modes, with the √N op and
+# SDPA timed beside it.
+CONFIGS = {
+    2: (1, 8, 64, "f16", (2048, 8192, 65536, 262144), "fwd"),
+    3: (1, 16, 128, "f16", (16384, 131072, 524288), "fwd"),
+    4: (1, 12, 64, "f16", (8192, 32768, 131072), "train"),
+    5: (2, 32, 128, "bf16", (512, 1024, 2048, 4096, 65536, 262144), "hybrid"),
+}
+# The reference's published forward / training ms on an RTX 5070 Ti (context
+# only: other hardware; README.md:23-80, 97-107). Config 5 is published at
+# B=1 only and config 4 (H=12) has no training figure.
+REFERENCE_MS = {
+    (2, 2048): 0.048, (2, 8192): 0.102, (2, 65536): 2.35, (2, 262144): 17.3,
+    (3, 16384): 1.25, (3, 131072): 27.6, (3, 524288): 191.0,
+    (5, 512): 0.052, (5, 1024): 0.070, (5, 2048): 0.132, (5, 4096): 0.242, (5, 65536): 17.0,
+    (5, 262144): 125.0,
+}
+
+
+def roofline_ms(B, H, S, D, esize, train: bool):
+    """max(F / MFMA peak, compulsory bytes / HBM peak) in ms, and the bound."""
+    P = pairs_fast(S)
+    F = (14 if train else 4) * D * P * B * H
+    nbytes = B * H * ((12 if train else 4) * S * D * esize + (8 if train else 4) * S)
+    t_f = F / (PEAK_FP16_TFLOPS * 1e12) * 1e3
+    t_b = nbytes / (PEAK_HBM_GBS * 1e9) * 1e3
+    return max(t_f, t_b), ("mfma" if t_f >= t_b else "hbm"), F
+
+
+def run_configs(args):
+    """Times every S of the selected BASELINE configurations: ms, effective
+    TFLOP/s, the fraction of the MFMA/HBM roofline and the 50% target; one
+    JSON line per point."""
+    import torch
+    import torch.nn.functional as F
+    import cron_root_attention as cra
+    from cron_root_attention.hybrid import dispatch_backend
+    dev = torch.device("cuda", 0)
+    sel = sorted(CONFIGS) if args.config == "all" else [int(x) for x in args.config.split(",")]
+    for c in sel:
+        B, H, D, dts, seqs, mode = CONFIGS[c]
+        dtype = {"f16": torch.float16, "bf16": torch.bfloat16}[dts]
+        for S in seqs:
+            gen = torch.Generator(device=dev).manual_seed(0)
+            mk = lambda: torch.randn(B, H, S, D, generator=gen, device=dev,
+                                     dtype=torch.float32).to(dtype)
+            q, k, v, dO = mk(), mk(), mk(), mk()
+            res = {"config": c, "B": B, "H": H, "D": D, "S": S, "dtype": dts, "mode": mode}
+
+            def fwd_ms(fn):
+                with torch.no_grad():
+                    return timed(lambda: fn(q, k, v), args.steps, args.warmup, torch)
+
+            def train_ms(fn):
+                qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+                def st():
+                    qg.grad = kg.grad = vg.grad = None
+                    fn(qg, kg, vg).backward(dO)
+                return timed(st, args.steps, args.warmup, torch)
+
+            cr = lambda a, b, cc: cra.cron_root_attention(a, b, cc)
+            for tr in ((False, True) if mode == "hybrid" else ((mode == "train"),)):
+                tag = "train" if tr else "fwd"
+                roof, bound, flops = roofline_ms(B, H, S, D, 2, tr)
+                t = train_ms(cr) if tr else fwd_ms(cr)
+                res[f"{tag}_ms"] = round(t, 4)
+                res[f"{tag}_tflops"] = round(flops / (t * 1e-3) / 1e12, 2)
+                res[f"{tag}_roofline_frac"] = round(roof / t, 4)
+                res[f"{tag}_bound"] = bound
+                res[f"{tag}_target_50pct_ms"] = round(2 * roof, 4)
+                if mode == "hybrid":
+                    backend = dispatch_backend(S, D, tr, B * H)
+                    res[f"{tag}_dispatch"] = backend
+                    if S <= 65536:
+                        sd = lambda a, b, cc: F.scaled_dot_product_attention(a, b, cc, is_causal=True)
+                        res[f"{tag}_sdpa_ms"] = round(train_ms(sd) if tr else fwd_ms(sd), 4)
+                    hy = lambda a, b, cc: cra.cron_root_attention_hybrid(a, b, cc)
+                    res[f"{tag}_hybrid_ms"] = round(train_ms(hy) if tr else fwd_ms(hy), 4)
+            ref = REFERENCE_MS.get((c, S))
+            if ref is not None:
+                res["reference_rtx5070ti_fwd_ms"] = ref
+            print(json.dumps(res), flush=True)
+            del q, k, v, dO
+            torch.cuda.empty_cache()
+
+
 def run_profile_workload(args):
     """Short fixed workload for counter passes (rocprofv3 --pmc): a 1 GiB
     device copy first (read 1 GiB + write 1 GiB, the calibration of
     FETCH_SIZE / WRITE_SIZE), then the hot path's kernels: build_global and
-    cra_fwd twice each, then one backward."""
+    cra_fwd twice each, the local-only and global-only forwards once each,
+    then one backward."""
     import torch
     from cron_root_attention import _native
     dev = torch.device("cuda", 0)
@@ -290,9 +431,113 @@ def run_profile_workload(args):
     for _ in range(2):
         gk, gv, src = _native.build_global(p, k, v, None)
         o, lse = _native.forward(p, q, k, v, gk, gv)
+    # the local-window and global-row phases on their own (their own kernels)
+    _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_LOCAL)
+    _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_GLOBAL)
     _native.backward(p, q, k, v, o, do, lse, gk, gv, src, None, False)
     torch.cuda.synchronize()
     print(json.dumps({"profile_workload": "done", "B": B, "H": H, "S": S, "D": D}), flush=True)
+
+
+def _demangle(name: str) -> str:
+    if not name.startswith("_Z"):
+        return name
+    import re
+    # this library's kernels: cra::(anon)::<kernel><template args>(args struct);
+    # decoded here because c++filt may not know the _Float16 (DF16_) mangling
+    m = re.match(r"_ZN3cra12_GLOBAL__N_1(\d+)(\w+)", name)
+    if m:
+        n = int(m.group(1))
+        kname, rest = m.group(2)[:n], m.group(2)[n:]
+        if rest.startswith("I"):
+            targs = []
+            for t in re.finditer(r"DF16_|DF16b|L[ib](\d+)E|(?<![A-Za-z])f(?=[LE])", rest[1:]):
+                tok = t.group(0)
+                targs.append({"DF16_": "f16", "DF16b": "bf16", "f": "f32"}.get(
+                    tok, "true" if tok == "Lb1E" else "false" if tok == "Lb0E" else t.group(1)))
+            return f"{kname}<{', '.join(targs)}>()"
+        return kname + "()"
+    import subprocess
+    try:
+        out = subprocess.run(["c++filt", name], capture_output=True, text=True, timeout=10)
+        return out.stdout.strip() or name
+    except (OSError, subprocess.SubprocessError):
+        return name
+
+
+def _short_kernel(name: str) -> str:
+    """'void cra::(anonymous namespace)::fwd2_kernel<_Float16, 128, 4, 3>(cra::FwdArgs)'
+    -> 'fwd2_kernel<_Float16, 128, 4, 3>'; torch kernels -> their template head."""
+    import re
+    name = _demangle(name)
+    m = re.search(r"(\w+_kernel)(<[^()]*>)?\(", name)
+    if m:
+        return m.group(1) + (m.group(2) or "")
+    return name[:60]
+
+
+def counter_summary(dirs, cus: int = 256, xcds: int = 8):
+    """Markdown summary of rocprofv3 --pmc passes (run_counter_collection.csv
+    under each directory) over --profile-workload: per kernel, the mean of
+    every counter over its dispatches and the derived figures."""
+    import csv
+    import glob
+    from collections import defaultdict
+    vals = defaultdict(lambda: defaultdict(list))   # kernel -> counter -> [per dispatch]
+    dur = defaultdict(list)
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f) as fh:
+                per = defaultdict(float)
+                meta = {}
+                for r in csv.DictReader(fh):
+                    key = (r["Dispatch_Id"], r["Counter_Name"])
+                    per[key] += float(r["Counter_Value"])
+                    meta[r["Dispatch_Id"]] = (_short_kernel(r["Kernel_Name"]),
+                                              int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+                for (disp, cn), v in per.items():
+                    kname, ns = meta[disp]
+                    vals[kname][cn].append(v)
+                    if cn in ("SQ_INSTS_MFMA", "FETCH_SIZE"):
+                        dur[kname].append(ns)
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    rows = []
+    copy_fetch = None
+    for k, c in vals.items():
+        if "copy" in k.lower() or "direct_copy" in k.lower():
+            copy_fetch = (mean(c.get("FETCH_SIZE", [])), mean(c.get("WRITE_SIZE", [])))
+    lines = ["| kernel | dispatches | MFMA busy | VALU / MFMA | trans / MFMA | SALU / MFMA | LDS / MFMA "
+             "| LDS bank-conflict cycles / LDS instr | wave time waiting | clock (GHz) "
+             "| read MB | written MB |",
+             "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    for k in sorted(vals, key=lambda x: -mean(dur.get(x, [0]))):
+        c = {n: mean(v) for n, v in vals[k].items()}
+        mf = c.get("SQ_INSTS_MFMA", 0)
+        if not mf:
+            continue
+        grbm = c.get("GRBM_GUI_ACTIVE")
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES")
+        util = busy / (grbm / xcds * cus * 4) if (grbm and busy) else float("nan")
+        ghz = (grbm / xcds) / mean(dur[k]) if grbm and dur.get(k) else float("nan")
+        wait = c.get("SQ_WAIT_ANY", 0) / c["SQ_WAVE_CYCLES"] if c.get("SQ_WAVE_CYCLES") else float("nan")
+        rd = c.get("FETCH_SIZE", float("nan")) * 1024 * 2 / 1e6   # FETCH_SIZE counts half the bytes read
+        wr = c.get("WRITE_SIZE", float("nan")) * 1024 / 1e6
+        lines.append(
+            f"| `{k}` | {len(vals[k]['SQ_INSTS_MFMA'])} | {util:.1%} | {c.get('SQ_INSTS_VALU', 0) / mf:.2f} "
+            f"| {c.get('SQ_INSTS_VALU_TRANS_F32', 0) / mf:.2f} | {c.get('SQ_INSTS_SALU', 0) / mf:.2f} "
+            f"| {c.get('SQ_INSTS_LDS', 0) / mf:.2f} "
+            f"| {c.get('SQ_LDS_BANK_CONFLICT', 0) / max(1.0, c.get('SQ_INSTS_LDS', 0)):.2f} "
+            f"| {wait:.1%} | {ghz:.2f} | {rd:.1f} | {wr:.1f} |")
+    extra = ["", "Raw means per dispatch (every counter of every pass):", "",
+             "| kernel | counter | mean per dispatch |", "|---|---|---|"]
+    for k in sorted(vals):
+        for n in sorted(vals[k]):
+            extra.append(f"| `{k}` | {n} | {mean(vals[k][n]):.6g} |")
+    cal = ""
+    if copy_fetch:
+        cal = (f"\nCalibration (1 GiB device copy of the same run): FETCH_SIZE {copy_fetch[0]:.0f} KiB, "
+               f"WRITE_SIZE {copy_fetch[1]:.0f} KiB per GiB moved.\n")
+    return "\n".join(lines) + "\n" + cal + "\n".join(extra) + "\n"
 
 
 def sdpa_backend(q, k, v, torch, F):
@@ -376,16 +621,26 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true", help="omit the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="CPU baseline threads (default: OMP_NUM_THREADS, else all allowed CPUs)")
     ap.add_argument("--crossover", action="store_true")
+    ap.add_argument("--config", default=None, metavar="N[,N]|all",
+                    help="time the BASELINE configurations 2-5 at every listed S instead")
     ap.add_argument("--profile-workload", action="store_true",
                     help="copy calibration + hot-path kernels once, for counter passes")
+    ap.add_argument("--counter-summary", nargs="+", metavar="DIR",
+                    help="print a markdown summary of rocprofv3 --pmc output directories")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "sharding across GPUs is design-only", file=sys.stderr)
         return 2
-    if args.crossover:
+    if args.counter_summary:
+        print(counter_summary(args.counter_summary))
+        return 0
+    if args.config:
+        run_configs(args)
+    elif args.crossover:
         run_crossover(args)
     elif args.profile_workload:
         run_profile_workload(args)

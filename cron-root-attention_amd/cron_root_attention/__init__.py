@@ -21,22 +21,33 @@ from . import _native
 
 
 def calibrate(H: int = 8, D: int = 64, dtype=None, S: int = 4096, verbose: bool = True) -> dict:
-    """Warm the kernels once for (H, D) (reference __init__.py:84-180).
+    """Report the kernel configuration for (H, D) (reference __init__.py:84-180).
 
     The reference benchmarks Triton (num_warps, num_stages) candidates here.
-    The HIP kernels have one compiled tile configuration per (dtype, D), so
-    this runs one forward+backward at S and reports that configuration.
+    The HIP kernels have one tile geometry per (dtype, D), fixed at build
+    time; this returns it as the library reports it (``cra_tile_config``),
+    in the reference's shape {"fwd": (warps, block), "bwd": (warps, block)}
+    plus the full geometry, and, on a GPU, runs one forward+backward at S to
+    load the kernels.
     """
     dtype = dtype or _torch.float16
-    dev = _torch.device("cuda", _torch.cuda.current_device())
-    q = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
-    k = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
-    v = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
-    cron_root_attention_v14(q, k, v).sum().backward()
-    _torch.cuda.synchronize(dev)
-    cfg = {"fwd": ("wave64x4", "q128"), "bwd": ("wave64x4", "k128")}
+    Dp = next((d for d in (32, 64, 128) if D <= d), D)
+    t = _native.tile_config(dtype, Dp)
+    if _torch.cuda.is_available():
+        dev = _torch.device("cuda", _torch.cuda.current_device())
+        q = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
+        k = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
+        v = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
+        cron_root_attention_v14(q, k, v).sum().backward()
+        _torch.cuda.synchronize(dev)
+    cfg = {"fwd": (t["fwd_waves"], t["fwd_queries"]), "bwd": (t["dq_waves"], t["dq_queries"]),
+           "tiles": t, "head_dim": Dp, "dtype": str(dtype).split(".")[-1]}
     if verbose:
-        print(f"  H={H} D={D}: fwd={cfg['fwd']} bwd={cfg['bwd']} (static gfx950 tiles)")
+        print(f"  H={H} D={D}: fwd {t['fwd_waves']} waves x {t['fwd_queries']} queries, "
+              f"{t['fwd_key_tile']}-key tiles; dQ {t['dq_waves']} waves x {t['dq_queries']} queries; "
+              f"global-row dK/dV {t['dkdv_global_waves']} waves x {t['dkdv_global_rows']} rows; "
+              f"local dK/dV {t['dkdv_local_waves']} waves x {t['dkdv_local_keys']} keys "
+              f"(static gfx950 tiles)")
     return cfg
 
 

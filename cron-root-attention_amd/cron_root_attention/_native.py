@@ -85,6 +85,13 @@ class CraDeviceInfo(ctypes.Structure):
                 ("arch_name", ctypes.c_char * 64), ("device_name", ctypes.c_char * 128)]
 
 
+class CraTileConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "fwd_waves", "fwd_queries", "fwd_key_tile", "dq_waves", "dq_queries", "dq_key_tile",
+        "dkdv_global_waves", "dkdv_global_rows", "dkdv_global_query_tile",
+        "dkdv_local_waves", "dkdv_local_keys", "dkdv_local_query_tile")]
+
+
 # Exported symbols and their signatures (mirrors include/cra.h).
 _P = ctypes.POINTER(CraProblem)
 _D = ctypes.POINTER(CraDocs)
@@ -122,6 +129,8 @@ _SIGNATURES = {
                                       CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
                                       ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "cra_device_info": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(CraDeviceInfo)]),
+    "cra_tile_config": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.POINTER(CraTileConfig)]),
     "cra_strerror": (ctypes.c_char_p, [ctypes.c_int32]),
     "cra_last_error": (ctypes.c_char_p, []),
     "cra_abi_version": (ctypes.c_int32, []),
@@ -357,6 +366,14 @@ def backward_varlen(p: CraProblem, docs: Docs, q, k, v, o, do, lse, gk, gv, src,
                               dalpha.data_ptr() if dalpha is not None else None, ws.data_ptr(),
                               ws.numel(), _stream(q)), "cra_bwd_varlen")
     return dq, dk, dv, dalpha
+
+
+def tile_config(dtype: torch.dtype, D: int) -> dict:
+    """The compiled tile geometry for (dtype, D) (cra_tile_config)."""
+    lib = load_library()
+    out = CraTileConfig()
+    _check(lib.cra_tile_config(dtype_code(dtype), D, ctypes.byref(out)), "cra_tile_config")
+    return {n: getattr(out, n) for n, _ in CraTileConfig._fields_}
 
 
 def device_info(index: int = 0) -> dict:

@@ -509,6 +509,28 @@ int cra_device_info(int32_t device, cra_device_info_t* out) {
   return CRA_OK;
 }
 
+int cra_tile_config(int32_t dtype, int32_t D, cra_tile_config_t* out) {
+  if (!out) return fail(CRA_E_INVALID, "out is NULL");
+  if (dtype != CRA_F16 && dtype != CRA_BF16 && dtype != CRA_F32)
+    return fail(CRA_E_DTYPE, "unknown dtype code %d", dtype);
+  int f[3], b[9];
+  if (!cra::fwd_tile_config(dtype, D, f) || !cra::bwd_tile_config(dtype, D, b))
+    return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128)", D);
+  out->fwd_waves = f[0];
+  out->fwd_queries = f[1];
+  out->fwd_key_tile = f[2];
+  out->dq_waves = b[0];
+  out->dq_queries = b[1];
+  out->dq_key_tile = b[2];
+  out->dkdv_global_waves = b[3];
+  out->dkdv_global_rows = b[4];
+  out->dkdv_global_query_tile = b[5];
+  out->dkdv_local_waves = b[6];
+  out->dkdv_local_keys = b[7];
+  out->dkdv_local_query_tile = b[8];
+  return CRA_OK;
+}
+
 const char* cra_strerror(int32_t code) {
   switch (code) {
     case CRA_OK: return "ok";

@@ -1366,6 +1366,22 @@ size_t bwd_workspace_layout(int D, int B, int Hq, int Hkv, int S, int64_t G, int
   return delta + part;
 }
 
+bool bwd_tile_config(int dtype, int D, int out[9]) {
+  if (dtype < 0 || dtype > 2 || (D != 32 && D != 64 && D != 128)) return false;
+  if (dtype == 2) {
+    using Tr = BwdTraits<float, 128>;
+    const int waves = Tr::kThreads / 64;
+    const int v[9] = {waves, Tr::kBM, Tr::kBN, waves, Tr::kBK, Tr::kBQ, waves, Tr::kBK, Tr::kBQ};
+    for (int i = 0; i < 9; ++i) out[i] = v[i];
+  } else {
+    const int v[9] = {kDqWaves,       16 * kDqWaves * kDqQB,           kDqBN,
+                      kDkdvGlobWaves, 16 * kDkdvGlobWaves * kDkdvKB,   kDkdvGlobBQ,
+                      kDkdvLocalWaves, 16 * kDkdvLocalWaves * kDkdvKB, kDkdvLocalBQ};
+    for (int i = 0; i < 9; ++i) out[i] = v[i];
+  }
+  return true;
+}
+
 hipError_t launch_bwd(int dtype, int D, const BwdArgs& a, hipStream_t st) {
   switch (dtype) {
     case 0: return launch_T<f16>(D, a, st);

@@ -626,6 +626,17 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
 }  // namespace
 
 
+bool fwd_tile_config(int dtype, int D, int out[3]) {
+  if (dtype < 0 || dtype > 2 || (D != 32 && D != 64 && D != 128)) return false;
+  if (dtype == 2) {
+    using Tr = FwdTraits<float, 128>;
+    out[0] = Tr::kWaves; out[1] = Tr::kBM; out[2] = Tr::kBN;
+  } else {
+    out[0] = kFwdWaves; out[1] = 32 * kFwdWaves; out[2] = 64;
+  }
+  return true;
+}
+
 hipError_t launch_fwd(int dtype, int D, const FwdArgs& a, hipStream_t st) {
   switch (dtype) {
     case 0: return launch_T<f16>(D, a, st);

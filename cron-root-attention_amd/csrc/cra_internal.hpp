@@ -114,6 +114,12 @@ __host__ __device__ inline int chunk_len_for(int len, int nchunk) {
   return (c + 63) / 64 * 64;
 }
 
+// Compiled tile geometry (dtype 0 f16, 1 bf16, 2 f32; D 32/64/128): the forward's
+// {waves, queries, key rows per tile} and the backward's {waves, rows, tile} of
+// dQ, global-row dK/dV and local dK/dV. Returns false for an unbuilt (dtype, D).
+bool fwd_tile_config(int dtype, int D, int out[3]);
+bool bwd_tile_config(int dtype, int D, int out[9]);
+
 // dtype: 0 f16, 1 bf16, 2 f32. Each returns hipError_t of the launch.
 hipError_t launch_build_global(int dtype, int D, const GlobalArgs& a, int B, hipStream_t st);
 hipError_t launch_fwd(int dtype, int D, const FwdArgs& a, hipStream_t st);

@@ -209,6 +209,20 @@ int cra_bwd_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor q, cra
  * __init__.py:183-202). */
 int cra_device_info(int32_t device, cra_device_info_t* out);
 
+/* The tile geometry compiled for (dtype, D): waves per workgroup, rows per
+ * workgroup (queries or key rows) and rows per streamed tile of the forward
+ * and the three backward kernels. Serves calibrate(), which in the reference
+ * times Triton (num_warps, num_stages) candidates per (op, H, D)
+ * (_KernelAutoTuner, core.py:250-596; __init__.py:84-180); here the
+ * geometry is fixed per (gfx950, dtype, D) at build time. */
+typedef struct {
+  int32_t fwd_waves, fwd_queries, fwd_key_tile;
+  int32_t dq_waves, dq_queries, dq_key_tile;
+  int32_t dkdv_global_waves, dkdv_global_rows, dkdv_global_query_tile;
+  int32_t dkdv_local_waves, dkdv_local_keys, dkdv_local_query_tile;
+} cra_tile_config_t;
+int cra_tile_config(int32_t dtype, int32_t D, cra_tile_config_t* out);
+
 const char* cra_strerror(int32_t code);
 const char* cra_last_error(void);
 int32_t cra_abi_version(void);

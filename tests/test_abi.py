@@ -234,3 +234,25 @@ def test_bwd_noalloc_rejects_problems_beyond_its_scratch():
     rc = lib.cra_bwd_noalloc(ctypes.byref(prob(top_k=9)), t, t, t, t, t, 0x10000, 0x10000,
                              0x10000, 0x10000, None, t, t, t, None, None)
     assert rc == N.E_INVALID
+
+
+def test_tile_config_reports_compiled_geometry():
+    """cra_tile_config (serves calibrate()): the geometry of the kernels as
+    built; a workgroup's rows are waves x rows per wave."""
+    import torch
+    for dt in (torch.float16, torch.bfloat16, torch.float32):
+        for D in (32, 64, 128):
+            t = N.tile_config(dt, D)
+            assert all(v > 0 for v in t.values())
+            assert t["fwd_queries"] == 32 * t["fwd_waves"]
+    h = N.tile_config(torch.float16, 128)
+    assert (h["fwd_waves"], h["fwd_queries"], h["fwd_key_tile"]) == (4, 128, 64)
+    assert (h["dkdv_global_waves"], h["dkdv_global_rows"]) == (12, 192)
+    assert (h["dkdv_local_waves"], h["dkdv_local_keys"], h["dkdv_local_query_tile"]) == (4, 64, 32)
+    lib = N.load_library()
+    out = N.CraTileConfig()
+    assert lib.cra_tile_config(0, 48, ctypes.byref(out)) == N.E_UNSUPPORTED
+    assert lib.cra_tile_config(9, 64, ctypes.byref(out)) == N.E_DTYPE
+    import cron_root_attention as cra
+    cfg = cra.calibrate(16, 128, verbose=False)
+    assert cfg["fwd"] == (4, 128) and cfg["tiles"] == h
