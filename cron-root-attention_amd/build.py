@@ -1,9 +1,10 @@
 """Build libcra_hip.so (gfx950) from csrc/ with hipcc.
 
 Usage: ``python cron-root-attention_amd/build.py [--jobs N] [--verbose]``.
-Each ``csrc/*.hip`` is compiled to an object under ``_build/`` and the
-objects are linked into ``cron_root_attention/libcra_hip.so`` next to the
-Python package that loads it.  Every call recompiles (the build is the
+Each ``csrc/*.hip`` is compiled with hipcc and each host-only ``csrc/*.cpp``
+(the CPU-tensor path) with the system C++ compiler to an object under
+``_build/``; the objects are linked into ``cron_root_attention/libcra_hip.so``
+next to the Python package that loads it.  Every call recompiles (the build is the
 "does it build" check); it takes well under a minute.
 """
 from __future__ import annotations
@@ -32,6 +33,10 @@ def hipcc() -> str:
     if not found:
         raise RuntimeError("hipcc not found (set ROCM_PATH)")
     return found
+
+
+def cxx() -> str:
+    return os.environ.get("CXX") or shutil.which("g++") or shutil.which("c++") or "g++"
 
 
 def common_flags() -> list[str]:
@@ -74,13 +79,19 @@ def build(jobs: int | None = None, verbose: bool = False, build_dir: str | None 
         obj = os.path.join(build_dir, s.replace(".hip", ".o"))
         objs.append(obj)
         cmds.append([cc, *common_flags(), "-c", os.path.join(CSRC, s), "-o", obj])
+    # host-only C++ (the CPU-tensor path): the system C++ compiler, no GPU code
+    for s in sorted(f for f in os.listdir(CSRC) if f.endswith(".cpp")):
+        obj = os.path.join(build_dir, s.replace(".cpp", ".cpp.o"))
+        objs.append(obj)
+        cmds.append([cxx(), "-O3", "-std=c++17", "-fPIC", "-pthread", "-Wall",
+                     "-c", os.path.join(CSRC, s), "-o", obj])
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for f in [ex.submit(run, c, verbose) for c in cmds]:
             f.result()
     out = os.path.join(OUT_DIR, LIB_NAME)
     tmp = out + ".tmp"
-    run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", tmp, *objs], verbose)
     os.replace(tmp, out)
     if verbose:
         print(f"built {out} in {time.time() - t0:.1f}s", flush=True)

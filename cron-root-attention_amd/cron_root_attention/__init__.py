@@ -23,12 +23,13 @@ from . import _native
 def calibrate(H: int = 8, D: int = 64, dtype=None, S: int = 4096, verbose: bool = True) -> dict:
     """Report the kernel configuration for (H, D) (reference __init__.py:84-180).
 
-    The reference benchmarks Triton (num_warps, num_stages) candidates here.
-    The HIP kernels have one tile geometry per (dtype, D), fixed at build
-    time; this returns it as the library reports it (``cra_tile_config``),
-    in the reference's shape {"fwd": (warps, block), "bwd": (warps, block)}
-    plus the full geometry, and, on a GPU, runs one forward+backward at S to
-    load the kernels.
+    The reference benchmarks Triton (num_warps, num_stages) candidates here
+    and returns {"fwd": (num_warps, num_stages), "bwd": (...)}. The HIP
+    kernels have one tile geometry per (dtype, D), fixed at build time; this
+    returns the same shape of dict with (waves per workgroup, LDS pipeline
+    stages) of the forward and of the dQ kernel, as the library reports them
+    (``cra_tile_config``; the whole geometry: ``_native.tile_config``), and,
+    on a GPU, runs one forward+backward at S to load the kernels.
     """
     dtype = dtype or _torch.float16
     Dp = next((d for d in (32, 64, 128) if D <= d), D)
@@ -40,14 +41,14 @@ def calibrate(H: int = 8, D: int = 64, dtype=None, S: int = 4096, verbose: bool 
         v = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
         cron_root_attention_v14(q, k, v).sum().backward()
         _torch.cuda.synchronize(dev)
-    cfg = {"fwd": (t["fwd_waves"], t["fwd_queries"]), "bwd": (t["dq_waves"], t["dq_queries"]),
-           "tiles": t, "head_dim": Dp, "dtype": str(dtype).split(".")[-1]}
+    stages = 2  # every kernel double-buffers its streamed tiles in LDS
+    cfg = {"fwd": (t["fwd_waves"], stages), "bwd": (t["dq_waves"], stages)}
     if verbose:
         print(f"  H={H} D={D}: fwd {t['fwd_waves']} waves x {t['fwd_queries']} queries, "
               f"{t['fwd_key_tile']}-key tiles; dQ {t['dq_waves']} waves x {t['dq_queries']} queries; "
               f"global-row dK/dV {t['dkdv_global_waves']} waves x {t['dkdv_global_rows']} rows; "
               f"local dK/dV {t['dkdv_local_waves']} waves x {t['dkdv_local_keys']} keys "
-              f"(static gfx950 tiles)")
+              f"(static gfx950 tiles, {stages} LDS stages)")
     return cfg
 
 

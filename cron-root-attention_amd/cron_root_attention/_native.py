@@ -131,6 +131,8 @@ _SIGNATURES = {
     "cra_device_info": (ctypes.c_int, [ctypes.c_int32, ctypes.POINTER(CraDeviceInfo)]),
     "cra_tile_config": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32,
                                        ctypes.POINTER(CraTileConfig)]),
+    "cra_fwd_cpu": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, CraTensor,
+                                   ctypes.c_int32]),
     "cra_strerror": (ctypes.c_char_p, [ctypes.c_int32]),
     "cra_last_error": (ctypes.c_char_p, []),
     "cra_abi_version": (ctypes.c_int32, []),
@@ -194,9 +196,28 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported dtype {dtype}; use float16, bfloat16 or float32") from None
 
 
+_problems = {}
+
+
 def problem(B, H_q, H_kv, S, D, W, relay, top_k, dtype, scale) -> CraProblem:
-    return CraProblem(B, H_q, H_kv, S, D, W, 1 if relay else 0, top_k if relay else 0,
-                      dtype_code(dtype), float(scale))
+    """The cra_problem of a call; one shared (read-only) instance per
+    distinct problem, with its derived sizes cached beside it."""
+    key = (B, H_q, H_kv, S, D, W, bool(relay), top_k if relay else 0, dtype, float(scale))
+    p = _problems.get(key)
+    if p is None:
+        p = CraProblem(B, H_q, H_kv, S, D, W, 1 if relay else 0, top_k if relay else 0,
+                       dtype_code(dtype), float(scale))
+        if len(_problems) > 4096:
+            _problems.clear()
+        _problems[key] = p
+    return p
+
+
+def _key(p: CraProblem):
+    return (p.B, p.H_q, p.H_kv, p.S, p.D, p.W, p.relay, p.top_k, p.dtype, p.scale)
+
+
+_sizes = {}
 
 
 def tensor_arg(t: torch.Tensor) -> CraTensor:
@@ -213,27 +234,31 @@ def supported_head_dim(D: int) -> bool:
 
 
 def global_rows(p: CraProblem) -> int:
-    n = load_library().cra_global_rows(ctypes.byref(p))
-    if n < 0:
-        _raise(E_INVALID, "cra_global_rows")
-    return int(n)
+    key = ("G",) + _key(p)
+    n = _sizes.get(key)
+    if n is None:
+        n = load_library().cra_global_rows(ctypes.byref(p))
+        if n < 0:
+            _raise(E_INVALID, "cra_global_rows")
+        n = _sizes[key] = int(n)
+    return n
 
 
 def build_global(p: CraProblem, k: torch.Tensor, v: torch.Tensor,
-                 relay_scale: Optional[torch.Tensor]):
+                 relay_scale: Optional[torch.Tensor], stream: Optional[int] = None):
     """Packed strided+relay rows (glob_k, glob_v) and relay source rows."""
     lib = load_library()
     G = global_rows(p)
     B, Hkv, D = p.B, p.H_kv, p.D
-    gk = torch.empty(B, Hkv, G, D, dtype=k.dtype, device=k.device)
-    gv = torch.empty_like(gk)
+    gkv = torch.empty(2, B, Hkv, G, D, dtype=k.dtype, device=k.device)  # one allocation
+    gk, gv = gkv[0], gkv[1]
     nb = (p.S + p.W - 1) // p.W
     src = (torch.empty(B, Hkv, nb * p.top_k, dtype=torch.int32, device=k.device)
            if p.relay else None)
     rs = relay_scale.data_ptr() if (relay_scale is not None and p.relay) else None
     _check(lib.cra_build_global(ctypes.byref(p), tensor_arg(k), tensor_arg(v), gk.data_ptr(),
                                 gv.data_ptr(), src.data_ptr() if src is not None else None, rs,
-                                _stream(k)), "cra_build_global")
+                                _stream(k) if stream is None else stream), "cra_build_global")
     return gk, gv, src
 
 
@@ -241,24 +266,30 @@ PHASE_LOCAL = 1
 PHASE_GLOBAL = 2
 
 
-def forward(p: CraProblem, q, k, v, gk, gv, phases: int = PHASE_LOCAL | PHASE_GLOBAL):
+def forward(p: CraProblem, q, k, v, gk, gv, phases: int = PHASE_LOCAL | PHASE_GLOBAL,
+            stream: Optional[int] = None):
     """cra_fwd (all phases) or cra_fwd_phases (a subset, for measurement)."""
     lib = load_library()
+    st = _stream(q) if stream is None else stream
     o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty(p.B, p.H_q, p.S, dtype=torch.float32, device=q.device)
     if phases == PHASE_LOCAL | PHASE_GLOBAL:
         _check(lib.cra_fwd(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
                            gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(),
-                           _stream(q)), "cra_fwd")
+                           st), "cra_fwd")
     else:
         _check(lib.cra_fwd_phases(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
                                   gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(),
-                                  phases, _stream(q)), "cra_fwd_phases")
+                                  phases, st), "cra_fwd_phases")
     return o, lse
 
 
 def workspace_bytes(p: CraProblem) -> int:
-    return int(load_library().cra_bwd_workspace_bytes(ctypes.byref(p)))
+    key = ("ws",) + _key(p)
+    n = _sizes.get(key)
+    if n is None:
+        n = _sizes[key] = int(load_library().cra_bwd_workspace_bytes(ctypes.byref(p)))
+    return n
 
 
 def backward(p: CraProblem, q, k, v, o, do, lse, gk, gv, src, relay_scale, want_dalpha: bool):
@@ -366,6 +397,15 @@ def backward_varlen(p: CraProblem, docs: Docs, q, k, v, o, do, lse, gk, gv, src,
                               dalpha.data_ptr() if dalpha is not None else None, ws.data_ptr(),
                               ws.numel(), _stream(q)), "cra_bwd_varlen")
     return dq, dk, dv, dalpha
+
+
+def forward_cpu(p: CraProblem, q, k, v, threads: int):
+    """cra_fwd_cpu: the host forward of CPU tensors (plan in p)."""
+    lib = load_library()
+    o = torch.empty(q.shape, dtype=q.dtype)
+    _check(lib.cra_fwd_cpu(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                           tensor_arg(o), max(1, int(threads))), "cra_fwd_cpu")
+    return o
 
 
 def tile_config(dtype: torch.dtype, D: int) -> dict:

@@ -12,8 +12,12 @@ logit scale 1/sqrt(D) (core.py:954).  The compute runs in libcra_hip.so:
 the three phases, ``cra_bwd`` produces dQ/dK/dV (and the relay-scale
 gradient).  Unlike the reference:
 
-* CPU tensors raise instead of running a CPU implementation (the reference
-  dispatches them to ``cra_cpu_fast_compiled``, core.py:3794-3796);
+* CPU tensors run the library's native host forward ``cra_fwd_cpu`` with the
+  plan of the reference's CPU path, ``cra_cpu_fast_compiled`` (core.py:3794-3796):
+  W = isqrt(S), relay always on, top 2 rows per block, GQA from the shapes,
+  ``kv_groups`` / ``relay_log_scale`` / ``relay_top_k`` / ``use_persistent``
+  ignored as there; it has no backward (the reference's CPU autograd fails on
+  its own in-place ops), so differentiating through it raises;
 * the backward returns fresh tensors (the reference returns static CUDA-graph
   buffers, core.py:3016-3020, 3367-3369) and runs on the caller's current
   stream (the reference replays on the default stream, core.py:3011);
@@ -173,8 +177,9 @@ class CronRootAttentionV14Function(torch.autograd.Function):
         p = _native.problem(B, Hq, Hkv, S, Dp, W, relay_on, relay_top_k, q.dtype,
                             1.0 / math.sqrt(D))
         rscale = _relay_scale(relay_log_scale, relay_on, q, Hkv)
-        gk, gv, src = _native.build_global(p, kp, vp, rscale)
-        o, lse = _native.forward(p, qp, kp, vp, gk, gv)
+        st = torch.cuda.current_stream(q.device).cuda_stream
+        gk, gv, src = _native.build_global(p, kp, vp, rscale, stream=st)
+        o, lse = _native.forward(p, qp, kp, vp, gk, gv, stream=st)
         ctx.problem = p
         ctx.D = D
         ctx.has_alpha = relay_log_scale is not None and relay_on
@@ -196,6 +201,44 @@ class CronRootAttentionV14Function(torch.autograd.Function):
         return dq, dk, dv, None, None, da, None, None, None
 
 
+class CronRootAttentionCPUFunction(torch.autograd.Function):
+    """Forward of CPU tensors (the reference's cra_cpu_fast plan, computed by
+    ``cra_fwd_cpu``); its backward raises."""
+
+    @staticmethod
+    def forward(ctx, q, k, v):
+        return _cpu_forward(q, k, v)
+
+    @staticmethod
+    def backward(ctx, do):
+        raise NotImplementedError(
+            "cron_root_attention has no backward for CPU tensors (neither has the "
+            "reference's CPU path); move q, k, v to a ROCm GPU to train")
+
+
+def _cpu_forward(q, k, v):
+    """CPU tensors: cra_cpu_fast's plan (cpu_reference.py:225-268) in native code."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be [B, H, S, D]")
+    B, Hq, S, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D:
+        raise ValueError(f"k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    Hkv = k.shape[1]
+    if Hq % Hkv:
+        raise ValueError(f"H_q={Hq} must be a multiple of H_kv={Hkv}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"unsupported dtype {q.dtype}; use float16, bfloat16 or float32")
+    if not (k.device.type == v.device.type == "cpu"):
+        raise ValueError("q, k, v must be on the same device")
+    qc, kc, vc = (t.detach() if t.stride(3) == 1 else t.detach().contiguous()
+                  for t in (q, k, v))
+    p = _native.problem(B, Hq, Hkv, S, D, max(1, math.isqrt(S)), True, 2, q.dtype,
+                        1.0 / math.sqrt(D))
+    return _native.forward_cpu(p, qc, kc, vc, torch.get_num_threads())
+
+
 @torch.compiler.disable
 def cron_root_attention_v14(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                             use_persistent: bool = False, kv_groups: int = 1,
@@ -213,7 +256,15 @@ def cron_root_attention_v14(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         relay_top_k: relay rows per sqrt(N) block (1..4).
 
     Returns: [B, H_q, S, D] in the dtype of q.
+
+    CPU tensors take the reference's CPU path (core.py:3794-3796): the plan of
+    ``cra_cpu_fast`` (W = isqrt(S), relay always on, top 2), computed by the
+    library's host code; forward only.
     """
+    if q.device.type == "cpu":
+        if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+            return CronRootAttentionCPUFunction.apply(q, k, v)
+        return _cpu_forward(q, k, v)
     return CronRootAttentionV14Function.apply(q, k, v, use_persistent, kv_groups,
                                               relay_log_scale, relay_top_k)
 

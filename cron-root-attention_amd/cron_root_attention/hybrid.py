@@ -7,8 +7,11 @@ forward and forward+backward separately: ``CROSSOVER_GFX950``.  Below a few
 thousand tokens the sqrt(N) op costs its launch floor (about 37 us forward,
 190-210 us forward+backward) while SDPA grows with B*H*S^2, so the crossover
 falls as B*H grows; the table keeps one row per measured B*H.
-``_SDPA_THRESHOLD`` is the forward+backward crossover at D=128 for B*H=16,
-the role of the reference's constant.  Both entry points default to
+The training floor is host-bound and moves with the host (the sqrt(N) op's
+forward+backward floor measured 0.10 and 0.18 ms on two boxes at B=1), so
+each row is the larger crossover of two boxes.  ``_SDPA_THRESHOLD`` is the
+forward+backward crossover at D=128 for B*H=16, the role of the reference's
+constant.  Both entry points default to
 ``threshold=None``, which looks the crossover up in the table for the call's
 head dim, B*H and grad mode; an integer threshold behaves as the reference's
 (S >= threshold runs the sqrt(N) op).
@@ -29,12 +32,13 @@ from .core import cron_root_attention_v14
 # shapes (B, H, D, dtype) = (1, 16, 128, fp16), (2, 32, 128, bf16),
 # (1, 8, 64, fp16), (1, 12, 64, fp16).
 CROSSOVER_GFX950 = {
-    ("fwd", 128, 1): 768,      # B=1 H=16 fp16 (fwd 0.037 vs 0.044 ms at S=768)
-    ("fwd", 128, 64): 512,     # B=2 H=32 bf16 (0.040 vs 0.041 ms at S=512)
-    ("train", 128, 1): 1536,   # B=1 H=16 fp16 (0.194 vs 0.324 ms at S=1536; 0.204 vs 0.200 at 1024)
-    ("train", 128, 64): 768,   # B=2 H=32 bf16 (0.193 vs 0.312 ms at S=768)
+    ("fwd", 128, 1): 768,      # B=1 H=16 fp16 (fwd 0.036 vs 0.044 ms at S=768)
+    ("fwd", 128, 64): 512,     # B=2 H=32 bf16 (0.039 vs 0.041 ms at S=512)
+    ("train", 128, 1): 1024,   # B=1 H=16 fp16 (0.18 vs 0.20 ms at S=1024 on the slower host;
+                               # 512 on the faster one)
+    ("train", 128, 64): 512,   # B=2 H=32 bf16 (0.189 vs 0.193 ms at S=512)
     ("fwd", 64, 1): 1536,      # B=1 H=8 and H=12 fp16
-    ("train", 64, 1): 2048,    # B=1 H=8 and H=12 fp16
+    ("train", 64, 1): 2048,    # B=1 H=8 and H=12 fp16 (768 on the faster host)
 }
 _SDPA_THRESHOLD = CROSSOVER_GFX950[("train", 128, 1)]
 

@@ -205,6 +205,20 @@ int cra_bwd_varlen(const cra_problem* p, const cra_docs* docs, cra_tensor q, cra
                    const float* relay_scale, cra_tensor dq, cra_tensor dk, cra_tensor dv,
                    float* dalpha, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Host (CPU) forward for CPU tensors: q, k, v, o are host memory in the
+ * layout above (any element strides, D contiguous). The attention
+ * set is the one above with p->W, p->relay and p->top_k, except that the
+ * relay rows of the last, partial block are chosen over the block padded
+ * with zero rows and relay rows are ranked by ||k||^2 rounded to the input
+ * dtype (earlier row first on equal norms). Arithmetic in fp32, one
+ * rounding of o to the input dtype; `threads` worker threads (>= 1).
+ * Replaces the reference's CPU dispatch `cra_cpu_fast_compiled(q, k, v)`
+ * (core.py:3794-3796; cra_cpu_fast, cpu_reference.py:198-339), whose plan
+ * the caller passes: W = isqrt(S), relay = 1, top_k = 2. No backward (the
+ * reference's CPU path has none that runs). */
+int cra_fwd_cpu(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+                int32_t threads);
+
 /* Device facts for get_num_sms()/get_gpu_info() (reference core.py:137-188,
  * __init__.py:183-202). */
 int cra_device_info(int32_t device, cra_device_info_t* out);

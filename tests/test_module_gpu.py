@@ -68,8 +68,8 @@ CFG5 = [512, 1024, 2048, 4096, 65536, 262144]
 @pytest.mark.parametrize("S", CFG5)
 def test_config5_module_hybrid(S, training):
     """B=2 H=32 D=128 bf16 through CronRootAttention(hybrid=True): the
-    dispatcher's choice per S (training crossover 768, inference 512 for
-    B*H = 64 on gfx950) and the result of whichever backend ran."""
+    dispatcher's choice per S (the gfx950 table's crossover for B*H = 64) and
+    the result of whichever backend ran."""
     B, H, D = 2, 32, 128
     E = H * D
     say(f"config 5 module hybrid S={S} {'train' if training else 'eval'}")
@@ -85,7 +85,6 @@ def test_config5_module_hybrid(S, training):
     with torch.no_grad():
         expect = "cron_root" if S >= crossover(D, training, B * H) else "sdpa"
         assert backend == expect
-        assert (S, training) != (512, True) or backend == "sdpa"
         assert S < 1024 or backend == "cron_root"
         attn = _heads(box[0], B, S, H, D)
         assert torch.equal(y, m.o_proj(box[0]))
@@ -249,6 +248,16 @@ def test_use_persistent_is_bit_identical(S):
         res.append((o.detach(), qd.grad, kd.grad, vd.grad))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("Hq,Hkv,kw", [(4, 2, {}), (4, 2, {"kv_groups": 3}), (3, 2, {"kv_groups": 1})])
+def test_kv_groups_validated_on_gpu(Hq, Hkv, kw):
+    """The GPU path takes the grouping from kv_groups (reference core.py:981)
+    and rejects shapes that disagree with it."""
+    q = torch.randn(1, Hq, 64, 32, device=DEV, dtype=F16)
+    k = torch.randn(1, Hkv, 64, 32, device=DEV, dtype=F16)
+    with pytest.raises(ValueError):
+        cra.cron_root_attention(q, k, k, **kw)
 
 
 def test_relay_log_scale_on_host_is_rejected():
