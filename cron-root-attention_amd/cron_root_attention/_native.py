@@ -105,6 +105,9 @@ _SIGNATURES = {
     "cra_fwd_phases": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
                                       ctypes.c_void_p, CraTensor, ctypes.c_void_p, ctypes.c_int32,
                                       ctypes.c_void_p]),
+    "cra_fwd_persistent": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, ctypes.c_void_p,
+                                          ctypes.c_void_p, CraTensor, ctypes.c_void_p,
+                                          ctypes.c_void_p, ctypes.c_void_p]),
     "cra_bwd_workspace_bytes": (ctypes.c_size_t, [_P]),
     "cra_bwd": (ctypes.c_int, [_P, CraTensor, CraTensor, CraTensor, CraTensor, CraTensor,
                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -281,6 +284,19 @@ def forward(p: CraProblem, q, k, v, gk, gv, phases: int = PHASE_LOCAL | PHASE_GL
         _check(lib.cra_fwd_phases(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
                                   gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(),
                                   phases, st), "cra_fwd_phases")
+    return o, lse
+
+
+def forward_persistent(p: CraProblem, q, k, v, gk, gv, stream: Optional[int] = None):
+    """cra_fwd_persistent: the work-queue forward (a zeroed counter per call)."""
+    lib = load_library()
+    o = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty(p.B, p.H_q, p.S, dtype=torch.float32, device=q.device)
+    counter = torch.zeros(1, dtype=torch.int32, device=q.device)
+    _check(lib.cra_fwd_persistent(ctypes.byref(p), tensor_arg(q), tensor_arg(k), tensor_arg(v),
+                                  gk.data_ptr(), gv.data_ptr(), tensor_arg(o), lse.data_ptr(),
+                                  counter.data_ptr(), _stream(q) if stream is None else stream),
+           "cra_fwd_persistent")
     return o, lse
 
 

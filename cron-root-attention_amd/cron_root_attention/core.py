@@ -26,9 +26,9 @@ gradient).  Unlike the reference:
 * with ``relay_log_scale`` the gradient reaching the relay source rows
   carries the exp(alpha) factor (the reference's scatter drops it,
   core.py:3541-3544 vs 3274-3290);
-* ``use_persistent`` is accepted and has no numerical effect, as in the
-  reference, whose persistent kernel computes the same no-relay function
-  (core.py:711-900): this build has one forward kernel for all S.
+* ``use_persistent`` on a sequence without relay (S <= 2048) runs the
+  persistent work-queue forward (``cra_fwd_persistent``), as the reference
+  does (core.py:3548-3569); the results are the tiled forward's, bit for bit.
 """
 from __future__ import annotations
 
@@ -179,7 +179,10 @@ class CronRootAttentionV14Function(torch.autograd.Function):
         rscale = _relay_scale(relay_log_scale, relay_on, q, Hkv)
         st = torch.cuda.current_stream(q.device).cuda_stream
         gk, gv, src = _native.build_global(p, kp, vp, rscale, stream=st)
-        o, lse = _native.forward(p, qp, kp, vp, gk, gv, stream=st)
+        if use_persistent and not relay_on:   # the reference's persistent path (core.py:3548)
+            o, lse = _native.forward_persistent(p, qp, kp, vp, gk, gv, stream=st)
+        else:
+            o, lse = _native.forward(p, qp, kp, vp, gk, gv, stream=st)
         ctx.problem = p
         ctx.D = D
         ctx.has_alpha = relay_log_scale is not None and relay_on
@@ -248,7 +251,8 @@ def cron_root_attention_v14(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
     Args:
         q: [B, H_q, S, D]; k, v: [B, H_kv, S, D] with H_q = H_kv * kv_groups.
-        use_persistent: accepted for compatibility; no numerical effect.
+        use_persistent: on sequences without relay (S <= 2048), run the
+            persistent work-queue forward (core.py:3548-3569); same results.
         kv_groups: query heads per kv head (query head h reads kv head
             h // kv_groups, core.py:981).
         relay_log_scale: optional [H_kv]; relay rows are scaled by

@@ -232,7 +232,7 @@ int build_global_impl(const cra_problem* p, const Plan& pl, cra_tensor k, cra_te
 
 int fwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, cra_tensor v,
              const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
-             int32_t phase_mask, void* stream) {
+             int32_t phase_mask, void* stream, int32_t* work_counter = nullptr) {
   if (phase_mask < 1 || phase_mask > (CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL))
     return fail(CRA_E_INVALID, "phase_mask must be a non-empty subset of CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL");
   const int esz = elem_size(p->dtype);
@@ -255,6 +255,7 @@ int fwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, c
   a.G = pl.G;
   a.scale = p->scale;
   a.phases = phase_mask;
+  a.work_counter = work_counter;
   for (int g = 0; g < num_groups(pl); ++g) {
     a.docs = group_table(pl, g);
     hipError_t e = cra::launch_fwd(p->dtype, p->D, a, (hipStream_t)stream);
@@ -405,6 +406,16 @@ int cra_fwd_phases(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor 
   Plan pl;
   if (int e = plan_plain(p, &pl)) return e;
   return fwd_impl(p, pl, q, k, v, glob_k, glob_v, o, lse, phase_mask, stream);
+}
+
+int cra_fwd_persistent(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+                       const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                       int32_t* work_counter, void* stream) {
+  Plan pl;
+  if (int e = plan_plain(p, &pl)) return e;
+  if (int e = check_buf("work_counter", work_counter)) return e;
+  return fwd_impl(p, pl, q, k, v, glob_k, glob_v, o, lse, CRA_PHASE_LOCAL | CRA_PHASE_GLOBAL,
+                  stream, work_counter);
 }
 
 size_t cra_bwd_workspace_bytes(const cra_problem* p) {

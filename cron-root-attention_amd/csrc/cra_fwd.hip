@@ -20,6 +20,7 @@
 // straight from the S^T registers. Tiles are launched heaviest first (work
 // per query grows with i) and consecutive workgroups are different heads of
 // the same tile, so each XCD keeps a fixed pair of heads.
+#include <algorithm>
 #include <type_traits>
 
 #include "cra_common.hpp"
@@ -424,24 +425,24 @@ __device__ __forceinline__ void attend_half(const char* tK, const char* tV, int 
 // of 174 allowed only 2: the D = 64 forward is 8% faster at 3). PH selects the key
 // phases (bit 0 local window, bit 1 global rows) at compile time, so the
 // phase-restricted launches are kernels of their own in a trace.
+template <int D>
+using FwdStage = char[2][SwzTile<D, 64>::kBytes];  // K and V tiles of one pipeline stage
+
+// One work item (a 128-query tile of one (b, h); items numbered heaviest
+// first, consecutive items on different heads) with its LDS stages.
 template <typename T, int D, int NW, int PH>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 3)))
-void fwd2_kernel(FwdArgs a) {
+__device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdStage<D>& stage0,
+                                          FwdStage<D>& stage1) {
   constexpr int BN = 64;
   using Tile = SwzTile<D, BN>;
   constexpr int kQW = 32, kBM = NW * kQW, kBN = BN;
-  // Two pipeline stages as separate LDS objects, each selected at compile
-  // time: the compiler can then tell the fill of one stage from reads of the
-  // other and does not wait for the fill before those reads.
-  __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];  // K, V
-  __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hq;
-  const int bh = blockIdx.x % nbh;
-  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  const int bh = item % nbh;
+  const Doc dc = find_doc(a.docs, item / nbh);
   const int tile = (dc.len + kBM - 1) / kBM - 1 - dc.item;  // heaviest first
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
@@ -583,6 +584,39 @@ void fwd2_kernel(FwdArgs a) {
   }
 }
 
+// Two pipeline stages as separate LDS objects, each selected at compile
+// time: the compiler can then tell the fill of one stage from reads of the
+// other and does not wait for the fill before those reads.
+template <typename T, int D, int NW, int PH>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 3)))
+void fwd2_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) FwdStage<D> stage0;
+  __shared__ __attribute__((aligned(1024))) FwdStage<D> stage1;
+  fwd2_item<T, D, NW, PH>(a, (int)blockIdx.x, stage0, stage1);
+}
+
+// Persistent form (use_persistent; the reference's work-queue kernel,
+// core.py:711-900): a grid of at most one round of resident workgroups, each
+// taking items in order (heaviest first) from a counter in device memory
+// that the caller zeroes, until none is left. Every workgroup ends once the
+// counter passes the item count.
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 3)))
+void fwd2_persistent_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) FwdStage<D> stage0;
+  __shared__ __attribute__((aligned(1024))) FwdStage<D> stage1;
+  __shared__ int next_item;
+  const int n_items = a.docs.item0[a.docs.n] * a.B * a.Hq;
+  for (;;) {
+    if (threadIdx.x == 0) next_item = atomicAdd(a.work_counter, 1);
+    __syncthreads();  // also: every wave is done with the previous item's LDS tiles
+    const int item = next_item;
+    __syncthreads();  // read before the next overwrite
+    if (item >= n_items) break;
+    fwd2_item<T, D, NW, 3>(a, item, stage0, stage1);
+  }
+}
+
 // Waves per forward workgroup (32 queries each) for 2-byte types. 8 waves
 // (256 queries sharing each K/V tile) halve the tile loads per query but
 // measured 4% slower at D = 128: the wider local window adds key tiles.
@@ -595,8 +629,23 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
     constexpr int kBM = 32 * kFwdWaves;
     set_items(b.docs, [&](int d) { return (b.docs.len[d] + kBM - 1) / kBM; });
     const dim3 grid(b.docs.item0[b.docs.n] * b.B * b.Hq), block(64 * kFwdWaves);
+    hipError_t qerr = hipSuccess;
     auto go = [&](auto dc) {
       constexpr int Dc = decltype(dc)::value;
+      if (a.work_counter && a.phases == 3) {
+        // one round of resident workgroups: CUs x workgroups per CU
+        auto kern = fwd2_persistent_kernel<T, Dc, kFwdWaves>;
+        int per_cu = 0, dev = 0, cus = 0;
+        qerr = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * kFwdWaves, 0);
+        if (qerr == hipSuccess) qerr = hipGetDevice(&dev);
+        if (qerr == hipSuccess)
+          qerr = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (qerr != hipSuccess) return;
+        const int items = (int)grid.x;
+        const dim3 pgrid(std::max(1, std::min(items, std::max(1, per_cu) * cus)));
+        hipLaunchKernelGGL(kern, pgrid, block, 0, st, b);
+        return;
+      }
       switch (a.phases) {
         case 1: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 1>), grid, block, 0, st, b); break;
         case 2: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 2>), grid, block, 0, st, b); break;
@@ -609,6 +658,7 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
       case 128: go(std::integral_constant<int, 128>{}); break;
       default: return hipErrorInvalidValue;
     }
+    if (qerr != hipSuccess) return qerr;
   } else {
     FwdArgs b = a;
     set_items(b.docs, [&](int d) { return (b.docs.len[d] + 127) / 128; });

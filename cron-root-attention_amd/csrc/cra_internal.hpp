@@ -64,6 +64,7 @@ struct FwdArgs {
   int64_t G;   // packed global rows of all documents, per head
   float scale;
   int phases;  // bit 0: local window, bit 1: global rows
+  int* work_counter;  // persistent launch: zeroed item counter, else null
   Docs docs;   // items: query tiles (set by the launcher for its tile size)
 };
 

@@ -99,10 +99,22 @@ int cra_build_global(const cra_problem* p, cra_tensor k, cra_tensor v, void* glo
  * (natural-log log-sum-exp per query). Query head h reads kv head
  * h / (H_q / H_kv).
  * Replaces the tiled forward `_cron_root_attn_fwd_v14_tiled`
- * (reference core.py:907-1158, launched at core.py:3588-3610) and the
- * persistent variant (core.py:711-900, launched at core.py:3548-3569). */
+ * (reference core.py:907-1158, launched at core.py:3588-3610). */
 int cra_fwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
             const void* glob_k, const void* glob_v, cra_tensor o, float* lse, void* stream);
+
+/* cra_fwd as a persistent kernel: a grid of one round of resident
+ * workgroups (CUs x workgroups per CU) that take the 128-query tiles, heaviest
+ * first, from the device counter *work_counter, which must be zero on entry
+ * (it ends at the number of tiles plus the number of workgroups; zero it
+ * again before the next call). Same results as cra_fwd, bit for bit (fp32
+ * inputs run cra_fwd's kernel). Replaces the reference's persistent forward
+ * `_cron_root_attn_fwd_v14_persistent` (core.py:711-900) with its atomic work
+ * queue, launched for use_persistent on sequences without relay
+ * (core.py:3548-3569). */
+int cra_fwd_persistent(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+                       const void* glob_k, const void* glob_v, cra_tensor o, float* lse,
+                       int32_t* work_counter, void* stream);
 
 /* Key phases for cra_fwd_phases. */
 #define CRA_PHASE_LOCAL 1  /* the local window [ls, i] */

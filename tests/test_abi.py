@@ -256,3 +256,11 @@ def test_tile_config_reports_compiled_geometry():
     import cron_root_attention as cra
     cfg = cra.calibrate(16, 128, verbose=False)
     assert cfg == {"fwd": (h["fwd_waves"], 2), "bwd": (h["dq_waves"], 2)}   # reference's keys
+
+
+def test_fwd_persistent_requires_a_counter():
+    lib = N.load_library()
+    t = N.CraTensor(0x10000, 1 << 20, 1 << 16, 128)
+    rc = lib.cra_fwd_persistent(ctypes.byref(prob(relay=0)), t, t, t, 0x10000, 0x10000, t,
+                                0x10000, None, None)
+    assert rc == N.E_INVALID and "work_counter" in lib.cra_last_error().decode()

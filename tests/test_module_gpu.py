@@ -129,7 +129,9 @@ def test_hybrid_function_dispatch(S):
 
 def test_hybrid_training_mode_uses_training_crossover():
     B, H, D = 1, 16, 128
-    S = 1024                    # fwd crossover 768 (sqrt(N)), training 1536 (SDPA)
+    thr_f, thr_t = crossover(D, False, B * H), crossover(D, True, B * H)
+    assert thr_f < thr_t
+    S = (thr_f + thr_t) // 2    # sqrt(N) for inference, SDPA for training
     q, k, v, do = inputs(B, H, H, S, D, F16, seed=2)
     qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
     out = cra.cron_root_attention_hybrid(qd, kd, vd)

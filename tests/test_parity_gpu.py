@@ -205,6 +205,24 @@ def test_backward_relay_log_scale():
     assert rel_fro(ad.grad, g["dalpha"]) <= 1e-4
 
 
+@pytest.mark.parametrize("dtype,B,H,S,D", [(F16, 1, 2, 1, 128), (F16, 2, 3, 700, 64),
+                                           (F16, 1, 16, 2048, 128), (BF16, 1, 4, 5000, 128),
+                                           (F16, 1, 2, 9000, 32), (F16, 1, 16, 131072, 128)])
+def test_persistent_forward_bit_identical(dtype, B, H, S, D):
+    """cra_fwd_persistent (work queue over a CU-sized grid) = cra_fwd, bit
+    for bit, with and without relay; a second call with a fresh counter too."""
+    say(f"persistent forward {dtype} B={B} H={H} S={S} D={D}")
+    q, k, v = device_inputs(B, H, H, S, D, dtype, seed=S)
+    plan = plan_for(S)
+    p = _native.problem(B, H, H, S, D, plan.W, plan.relay, 2, dtype, 1 / math.sqrt(D))
+    gk, gv, _ = _native.build_global(p, k, v, None)
+    o, lse = _native.forward(p, q, k, v, gk, gv)
+    for _ in range(2):
+        op, lsep = _native.forward_persistent(p, q, k, v, gk, gv)
+        torch.cuda.synchronize()
+        assert torch.equal(op, o) and torch.equal(lsep, lse)
+
+
 def test_backward_deterministic():
     B, H, S, D = 1, 4, 6000, 128
     q, k, v, do = inputs(B, H, H, S, D, F16, seed=9)
