@@ -87,28 +87,6 @@ __device__ __forceinline__ Frag<T> pack8(const float (&v)[8]) {
   return f;
 }
 
-// fp32 sum of the eight values of a 2-byte P fragment: exactly the values
-// the P.V MFMA multiplies (one v_dot2 with (1, 1) per pair; the products are
-// exact). Normalising by this sum makes O a convex combination of V rows with
-// the rounded weights, so the rounding of a dominant weight cancels in O.
-__device__ __forceinline__ float frag_sum(const Frag<f16>& f) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(f.w);
-  const f16x2 one = {(f16)1.f, (f16)1.f};
-  float acc = 0.f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w[s]), one, acc, false);
-  return acc;
-}
-__device__ __forceinline__ float frag_sum(const Frag<bf16>& f) {
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(f.w);
-  const bf16x2 one = {(bf16)1.f, (bf16)1.f};
-  float acc = 0.f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[s]), one, acc, false);
-  return acc;
-}
-
 // ---------------------------------------------------------------------------
 // LDS operand reads.
 // ---------------------------------------------------------------------------

@@ -306,16 +306,35 @@ __device__ __forceinline__ void pv_half(const char* tV, int kh, const Fwd2Lane<D
   }
 }
 
-// Largest sum of 8 exponentials accepted against the running maximum: each
-// term is then at most 2^15 and stays finite once rounded to fp16.
+// Largest sum of a half's 32 rounded exponentials accepted against the
+// running maximum: each term is then at most 2^15 and finite in fp16.
 constexpr float kSumMax = 32768.f;
+
+// All-ones A operand: ones . P^T puts the sum over the 32 keys of each query
+// (column of P^T) in all four of that query's lanes' result rows.
+template <typename T>
+__device__ __forceinline__ Frag<T> ones_frag() {
+  Frag<T> f;
+  const uint32_t w = sizeof(T) == 2 ? (std::is_same<T, bf16>::value ? 0x3f803f80u : 0x3c003c00u)
+                                    : 0u;
+  f.w[0] = make_uint4(w, w, w, w);
+  return f;
+}
+
+// Sum of the rounded P of a 32-key half for each query, on the matrix core
+// (one MFMA in place of four v_dot2 per lane plus a cross-lane sum).
+template <typename T>
+__device__ __forceinline__ float half_sum(const Frag<T>& pk, const Frag<T>& one) {
+  return mma(f32x4{0.f, 0.f, 0.f, 0.f}, one, pk)[0];
+}
 
 // Exponentials of one 32-key half (8 per lane and query block) against the
 // running maximum, rounded to the input type, and the sum of the rounded
-// values (the P.V operand and its normaliser).
+// values over the half's 32 keys (the P.V operand and its normaliser).
 template <typename T, bool MASK>
 __device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float c2, float m,
-                                         int g, const TileMask& mk, Frag<T>& pk, float& ps) {
+                                         int g, const TileMask& mk, const Frag<T>& one,
+                                         Frag<T>& pk, float& ps) {
   float pv[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -325,7 +344,7 @@ __device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float
       pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -m));
     }
   pk = pack8<T>(pv);
-  ps = frag_sum(pk);
+  ps = half_sum(pk, one);
 }
 
 // Raise the running maximum of query block qb to this half's maximum,
@@ -336,18 +355,23 @@ __device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float
 template <typename T, int D>
 __device__ __forceinline__ void half_rescale(f32x4 (&s)[2][2], int qb, float c2,
                                              f32x4 (&acc)[D / 16][2], float (&m_run)[2],
-                                             float (&l_run)[2], Frag<T>& pk, float& ps) {
+                                             float (&l_run)[2], const Frag<T>& one, Frag<T>& pk,
+                                             float& ps) {
   float mx = -__builtin_huge_valf();
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[h][qb][r]);
   const float m_new = fmaxf(m_run[qb], group_max(mx * c2));
-  const float alpha =
-      m_run[qb] == -__builtin_huge_valf() ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-  l_run[qb] *= alpha;
+  // Until a query's first visible key its accumulators and l are zero; the
+  // whole wave's first rescale (its first tile) has nothing to scale.
+  if (!__all(m_run[qb] == -__builtin_huge_valf())) {
+    const float alpha =
+        m_run[qb] == -__builtin_huge_valf() ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+    l_run[qb] *= alpha;
 #pragma unroll
-  for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
+    for (int db = 0; db < D / 16; ++db) acc[db][qb] *= alpha;
+  }
   m_run[qb] = m_new;
   const float mu = m_new == -__builtin_huge_valf() ? 0.f : m_new;
   float pv[8];
@@ -356,7 +380,7 @@ __device__ __forceinline__ void half_rescale(f32x4 (&s)[2][2], int qb, float c2,
 #pragma unroll
     for (int r = 0; r < 4; ++r) pv[4 * h + r] = __builtin_amdgcn_exp2f(fmaf(s[h][qb][r], c2, -mu));
   pk = pack8<T>(pv);
-  ps = frag_sum(pk);
+  ps = half_sum(pk, one);
 }
 
 // One BN-key tile for the wave's 32 queries, in 32-key halves. The online
@@ -370,7 +394,7 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
                                              const Frag<T> (&qf)[2][D / 32],
                                              f32x4 (&acc)[D / 16][2], float (&m_run)[2],
                                              float (&l_run)[2], float c2, int g,
-                                             const TileMask& mk) {
+                                             const TileMask& mk, const Frag<T>& one) {
   using Tile = SwzTile<D, BN>;
   constexpr int kHalves = BN / 32;
   f32x4 s[kHalves][2][2];
@@ -382,13 +406,13 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
     float ps[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
-      half_exp<T, MASK>(s[kc], kc, qb, c2, m_run[qb], g, mk, pn[qb], ps[qb]);
+      half_exp<T, MASK>(s[kc], kc, qb, c2, m_run[qb], g, mk, one, pn[qb], ps[qb]);
     if (kc > 0) pv_half<T, D, BN>(tV, kc - 1, lo, pf, acc);  // beside this half's exponentials
     if (kc + 1 < kHalves) tile_scores<T, D, BN>(tK, lo, qf, kc + 1, s[kc + 1]);
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       if (__any(!(ps[qb] <= kSumMax)))
-        half_rescale<T, D>(s[kc], qb, c2, acc, m_run, l_run, pn[qb], ps[qb]);
+        half_rescale<T, D>(s[kc], qb, c2, acc, m_run, l_run, one, pn[qb], ps[qb]);
       l_run[qb] += ps[qb];
       pf[qb] = pn[qb];
     }
@@ -403,17 +427,19 @@ __device__ __forceinline__ void attend_half(const char* tK, const char* tV, int 
                                             const Fwd2Lane<D>& lo, const Frag<T> (&qf)[2][D / 32],
                                             f32x4 (&acc)[D / 16][2], float (&m_run)[2],
                                             float (&l_run)[2], float c2, int g,
-                                            const TileMask& mk) {
+                                            const TileMask& mk, const Frag<T>& one) {
   using Tile = SwzTile<D, BN>;
   f32x4 s[2][2];
   tile_scores<T, D, BN>(tK, lo, qf, kc, s);
   float ps[2];
   Frag<T> pf[2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) half_exp<T, true>(s, kc, qb, c2, m_run[qb], g, mk, pf[qb], ps[qb]);
+  for (int qb = 0; qb < 2; ++qb)
+    half_exp<T, true>(s, kc, qb, c2, m_run[qb], g, mk, one, pf[qb], ps[qb]);
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    if (__any(!(ps[qb] <= kSumMax))) half_rescale<T, D>(s, qb, c2, acc, m_run, l_run, pf[qb], ps[qb]);
+    if (__any(!(ps[qb] <= kSumMax)))
+      half_rescale<T, D>(s, qb, c2, acc, m_run, l_run, one, pf[qb], ps[qb]);
     l_run[qb] += ps[qb];
   }
   pv_half<T, D, BN>(tV, kc, lo, pf, acc);
@@ -526,6 +552,7 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
   const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
   const int glen[2] = {glob_prefix(qi[0], W, rpb), glob_prefix(qi[1], W, rpb)};
 
+  const Frag<T> one = ones_frag<T>();
   // Local and global tiles share one body (parameters chosen per tile); the
   // loop is unrolled over the two stages.
   auto step = [&](auto stage_c, int it) {
@@ -553,11 +580,11 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
       const int vis_hi = loc ? q_last - ts : wg_hi - 1 - ts;
       const bool half0 = vis_lo <= 31, half1 = vis_hi >= 32;
       if (full)
-        attend_tile2<T, D, BN, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
+        attend_tile2<T, D, BN, false>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk, one);
       else if (half0 && half1)
-        attend_tile2<T, D, BN, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk);
+        attend_tile2<T, D, BN, true>(tK, tV, lo, qf, acc, m_run, l_run, c2, g, mk, one);
       else
-        attend_half<T, D, BN>(tK, tV, half0 ? 0 : 1, lo, qf, acc, m_run, l_run, c2, g, mk);
+        attend_half<T, D, BN>(tK, tV, half0 ? 0 : 1, lo, qf, acc, m_run, l_run, c2, g, mk, one);
     }
   };
   for (int it = 0; it < ntot; it += 2) {
@@ -568,9 +595,10 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
   T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    const float l = group_sum(l_run[qb]);
+    const float l = l_run[qb];  // each lane holds its query's whole sum
     if (!active || qi[qb] >= S) continue;
-    const float inv = 1.f / fmaxf(l, 1e-6f);
+    // O is rounded to the 2-byte type: the reciprocal's 1-ulp error is invisible
+    const float inv = __builtin_amdgcn_rcpf(fmaxf(l, 1e-6f));
     T* orow = op + (int64_t)qi[qb] * a.oss;
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
