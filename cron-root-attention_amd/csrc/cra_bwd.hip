@@ -930,9 +930,11 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
   // subtile's score MFMAs beside this one's exponentials, needs 225
   // registers and 2 waves per SIMD: 4.2% slower backward with the local
   // kernel.) LOC (local rows) tests each mask with one unsigned compare;
-  // the global-row kernel keeps two compares.
+  // the global-row kernel keeps two compares. Unrolled by two only: the four
+  // subtiles of a 128-row tile fully unrolled spill (the compiler hoists the
+  // next subtiles' fragment reads).
   f32x4 sc[2][KB], dp[2][KB];  // [qb2][kb]
-#pragma unroll
+#pragma unroll 2
   for (int qs = 0; qs < NS; ++qs) {
     scores(qs, sc, dp);
     float p[2][KB][4], ds[2][KB][4];  // [qb2][kb][r]
@@ -1266,8 +1268,10 @@ constexpr int kDqBN = 64;   // key rows per dQ tile
 constexpr int kDqWPE = 2;   // dQ waves per SIMD (register budget)
 // Query rows per dK/dV tile. The local kernel's 32-row tiles keep its LDS
 // at 33 KB, so three 4-wave workgroups (3 waves per SIMD, 160 VGPRs) fit on
-// a CU; with 64-row tiles only two fit.
-constexpr int kDkdvGlobBQ = 64;
+// a CU; with 64-row tiles only two fit. The global-row kernel (one 12-wave
+// workgroup per CU, 130 KB of LDS) takes 128-row tiles: one barrier per 128
+// queries instead of 64 (backward 1.7% faster).
+constexpr int kDkdvGlobBQ = 128;
 constexpr int kDkdvLocalBQ = 32;
 
 template <typename T, int D>
