@@ -490,7 +490,11 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
   const int nloc = (PH & 1) ? (hi - lo_k + kBN - 1) / kBN : 0;
   // Global tiles come first: every workgroup of the head reads them, so the
   // first fill (issued before anything can hide it) is an L2 hit, and the
-  // cold local rows are fetched while global tiles are computed.
+  // cold local rows are fetched while global tiles are computed. The local
+  // window is then walked from its highest key tile down: the workgroup of
+  // the next lower query tile (launched next for this head) walks down the
+  // same keys one or two tiles behind and finds them in L2 (the forward's HBM
+  // reads drop from 1.32 to 1.14 times the compulsory bytes).
   const int nglob = (PH & 2) ? (gmax + kBN - 1) / kBN : 0;
   const int ntot = nloc + nglob;
 
@@ -508,7 +512,7 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
   const int fg = Fill::lane_off(wave, lane, D * 2);
   auto issue = [&](int it, char* dst) {
     if (it >= nglob) {
-      const int ts = lo_k + (it - nglob) * kBN;
+      const int ts = lo_k + (nloc - 1 - (it - nglob)) * kBN;
       Fill::load(dst, rk, fk, kbytes, ts, wave);
       Fill::load(dst + Tile::kBytes, rv, fv, vbytes, ts, wave);
     } else {
@@ -565,7 +569,7 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
     const char* tK = cur[0];
     const char* tV = cur[1];
     const bool loc = it >= nglob;
-    const int ts = loc ? lo_k + (it - nglob) * kBN : it * kBN;
+    const int ts = loc ? lo_k + (nloc - 1 - (it - nglob)) * kBN : it * kBN;
     const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
     const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
     TileMask mk;
