@@ -170,6 +170,10 @@ BWD_CASES = [
     # 2-byte types at D = 32 (and 16, padded to 32): tiles whose fill takes
     # fewer instructions than the kernels have waves
     (F16, 1, 2, 2, 3000, 32, 2), (BF16, 1, 2, 2, 2100, 16, 2),
+    # a single query and a sequence shorter than one query tile; relay
+    # top-1 and top-3 in the 2-byte kernels; 8 query heads per kv head
+    (F16, 1, 2, 2, 1, 64, 2), (F16, 1, 2, 2, 33, 128, 2), (F16, 1, 2, 2, 4500, 128, 1),
+    (BF16, 1, 4, 2, 3500, 128, 3), (F16, 1, 8, 1, 2200, 128, 2),
 ]
 
 
@@ -184,6 +188,15 @@ def test_backward_matches_oracle(case):
     _, _, _, g = O.forward_backward(q, k, v, do, plan_for(S, top_k), kv_groups=Hq // Hkv)
     for name, hip, ref in (("dq", qd.grad, g["dq"]), ("dk", kd.grad, g["dk"]),
                            ("dv", vd.grad, g["dv"])):
+        if float(ref.norm()) <= 1e-9 * float(do.norm()):
+            # A single query with its single key (S = 1): P = 1 and dP equals
+            # Delta, so dQ = dK = 0 exactly; the kernels form Delta from the
+            # rounded O and return rounding-level values, for which a
+            # relative error is undefined.
+            m = float(hip.detach().abs().max())
+            say(f"  {name}: exact gradient is zero, max-abs = {m:.3e}")
+            assert m <= 1e-4, name
+            continue
         e = rel_fro(hip, ref)
         say(f"  {name}: rel = {e:.3e}")
         assert e <= TOL_GRAD[dtype], name
