@@ -993,9 +993,11 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
 }
 
 // NW waves of KB key blocks each cover the workgroup's 16 * NW * KB key
-// rows; query tiles of BQ rows. At most 168 VGPRs: 3 waves per SIMD.
+// rows; query tiles of BQ rows. At most 168 VGPRs: 3 waves per SIMD (the
+// global-row kernel below D = 128: at most 128, 4 waves per SIMD).
 template <typename T, int D, bool GLOB, int NW, int KB, int BQ>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(GLOB && D < 128 ? 4 : 3)))
 void dkdv2_kernel(BwdArgs a) {
   using Tile = SwzTile<D, BQ>;
   constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = BQ;
@@ -1261,7 +1263,12 @@ void dkdv2_kernel(BwdArgs a) {
 // fragment read from LDS serves two query blocks). 16 queries per wave
 // lose that reuse: 8 waves measured 27% slower, and with 32-key tiles at
 // 3 or 4 waves per SIMD still 5-10% slower backward at D = 128.
-constexpr int kDkdvGlobWaves = 12;
+// Below D = 128 the global-row kernel needs at most 128 VGPRs (112 at
+// D = 64), so two 8-wave workgroups share a CU at 4 waves per SIMD, where
+// one 12-wave workgroup left it at 3: backward 1.4% faster at B=1 H=12
+// S=131072 D=64 and 3.3% at H=8 S=65536 (16-wave workgroups: 0.8%).
+template <int D>
+constexpr int kDkdvGlobWaves = D == 128 ? 12 : 8;
 constexpr int kDkdvLocalWaves = 4;
 constexpr int kDkdvKB = 1;  // 16-key blocks per wave
 constexpr int kDqWaves = 4;
@@ -1291,7 +1298,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   constexpr int kQM = sizeof(T) == 2 ? 16 * kDqWaves * kDqQB : Tr::kBM;  // dQ queries per workgroup
   set_items(aq.docs, [&](int d) { return (a.docs.len[d] + kQM - 1) / kQM; });
   constexpr bool kMfma = sizeof(T) == 2;
-  constexpr int kGK = kMfma ? 16 * kDkdvGlobWaves * kDkdvKB : Tr::kBK;   // rows per workgroup
+  constexpr int kGK = kMfma ? 16 * kDkdvGlobWaves<D> * kDkdvKB : Tr::kBK;   // rows per workgroup
   constexpr int kLK = kMfma ? 16 * kDkdvLocalWaves * kDkdvKB : Tr::kBK;
   set_items(ag.docs, [&](int d) {
     const int g = (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d] * a.docs.rpb[d];
@@ -1303,8 +1310,8 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, kDqQB, kDqBN, kDqWPE>), dim3(nq * a.B * a.Hq),
                        dim3(64 * kDqWaves), 0, st, aq);
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvGlobWaves, kDkdvKB, kDkdvGlobBQ>),
-                       dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvGlobWaves), 0, st, ag);
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvGlobWaves<D>, kDkdvKB, kDkdvGlobBQ>),
+                       dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvGlobWaves<D>), 0, st, ag);
   } else {
     hipLaunchKernelGGL((dq_kernel<T, D>), dim3(nq * a.B * a.Hq), dim3(256), 0, st, aq);
     hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(ng * a.B * a.Hkv), dim3(256), 0, st, ag);
@@ -1380,8 +1387,9 @@ bool bwd_tile_config(int dtype, int D, int out[9]) {
     const int v[9] = {waves, Tr::kBM, Tr::kBN, waves, Tr::kBK, Tr::kBQ, waves, Tr::kBK, Tr::kBQ};
     for (int i = 0; i < 9; ++i) out[i] = v[i];
   } else {
-    const int v[9] = {kDqWaves,       16 * kDqWaves * kDqQB,           kDqBN,
-                      kDkdvGlobWaves, 16 * kDkdvGlobWaves * kDkdvKB,   kDkdvGlobBQ,
+    const int gw = D == 128 ? kDkdvGlobWaves<128> : kDkdvGlobWaves<64>;
+    const int v[9] = {kDqWaves,        16 * kDqWaves * kDqQB,           kDqBN,
+                      gw,              16 * gw * kDkdvKB,               kDkdvGlobBQ,
                       kDkdvLocalWaves, 16 * kDkdvLocalWaves * kDkdvKB, kDkdvLocalBQ};
     for (int i = 0; i < 9; ++i) out[i] = v[i];
   }

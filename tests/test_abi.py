@@ -248,6 +248,8 @@ def test_tile_config_reports_compiled_geometry():
     h = N.tile_config(torch.float16, 128)
     assert (h["fwd_waves"], h["fwd_queries"], h["fwd_key_tile"]) == (4, 128, 64)
     assert (h["dkdv_global_waves"], h["dkdv_global_rows"]) == (12, 192)
+    h64 = N.tile_config(torch.float16, 64)   # 4 waves per SIMD below D = 128
+    assert (h64["dkdv_global_waves"], h64["dkdv_global_rows"]) == (8, 128)
     assert (h["dkdv_local_waves"], h["dkdv_local_keys"], h["dkdv_local_query_tile"]) == (4, 64, 32)
     lib = N.load_library()
     out = N.CraTileConfig()
