@@ -266,23 +266,24 @@ __device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& l
                                             const Frag<T> (&qf)[2][D / 32], int kc,
                                             f32x4 (&s)[2][2]) {
   using Tile = SwzTile<D, BN>;
-  constexpr int NC = D / 32;
-  // K fragments are read one step ahead of the MFMAs that use them
-  Frag<T> kf[2];
-  kf[0] = Tile::template row_frag_at<T>(tK + (2 * kc) * Tile::kBlk16 + lo.k[0]);
+  constexpr int NC = D / 32, NK = 2 * NC;
+  // K fragments are read two steps ahead of the MFMAs that use them; fences
+  // keep the compiler from moving the reads next to their uses
+  auto k_frag = [&](int t) {
+    return Tile::template row_frag_at<T>(tK + (2 * kc + t / NC) * Tile::kBlk16 + lo.k[t % NC]);
+  };
+  Frag<T> kf[3];
+  kf[0] = k_frag(0);
+  kf[1] = k_frag(1);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    s[h][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    s[h][1] = s[h][0];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int t = h * NC + c;
-      if (t + 1 < 2 * NC)
-        kf[(t + 1) & 1] = Tile::template row_frag_at<T>(
-            tK + (2 * kc + (t + 1) / NC) * Tile::kBlk16 + lo.k[(t + 1) % NC]);
-      s[h][0] = mma(s[h][0], kf[t & 1], qf[0][c]);
-      s[h][1] = mma(s[h][1], kf[t & 1], qf[1][c]);
-    }
+  for (int t = 0; t < NK; ++t) {
+    if (t + 2 < NK) kf[(t + 2) % 3] = k_frag(t + 2);
+    const int h = t / NC, c = t % NC;
+    if (c == 0) s[h][0] = s[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s[h][0] = mma(s[h][0], kf[t % 3], qf[0][c]);
+    s[h][1] = mma(s[h][1], kf[t % 3], qf[1][c]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -292,17 +293,21 @@ template <typename T, int D, int BN>
 __device__ __forceinline__ void pv_half(const char* tV, int kh, const Fwd2Lane<D>& lo,
                                         const Frag<T> (&pf)[2], f32x4 (&acc)[D / 16][2]) {
   using Tile = SwzTile<D, BN>;
+  constexpr int NDB = D / 16;
   auto tr_v = [&](int db) {
     const char* pa = tV + (2 * kh) * Tile::kBlk16 + lo.v[db];
     return Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
   };
-  Frag<T> vt[2];
+  Frag<T> vt[3];
   vt[0] = tr_v(0);
+  vt[1] = tr_v(1);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int db = 0; db < D / 16; ++db) {
-    if (db + 1 < D / 16) vt[(db + 1) & 1] = tr_v(db + 1);
-    acc[db][0] = mma(acc[db][0], vt[db & 1], pf[0]);
-    acc[db][1] = mma(acc[db][1], vt[db & 1], pf[1]);
+  for (int db = 0; db < NDB; ++db) {
+    if (db + 2 < NDB) vt[(db + 2) % 3] = tr_v(db + 2);
+    acc[db][0] = mma(acc[db][0], vt[db % 3], pf[0]);
+    acc[db][1] = mma(acc[db][1], vt[db % 3], pf[1]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
