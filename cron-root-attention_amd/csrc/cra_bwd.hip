@@ -655,10 +655,18 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
     // masked tiles: a 32-key half with no key visible to the wave is skipped
     if (MASK && !(kc ? half1 : half0)) continue;
     float ds[2][QB][4];  // [h][qb][r]
-    // K and V row fragments are read one step ahead of their MFMAs
-    Frag<T> kf[2], vf[2];
-    kf[0] = Tile::template row_frag_at<T>(tK + (2 * kc) * Tile::kBlk16 + lo.row[0]);
-    vf[0] = Tile::template row_frag_at<T>(tV + (2 * kc) * Tile::kBlk16 + lo.row[0]);
+    // K and V row fragments are read two steps ahead of their MFMAs; fences
+    // keep the compiler from moving the reads next to their uses
+    constexpr int NT = 2 * NC;
+    auto row_kv = [&](int t, Frag<T>& k_, Frag<T>& v_) {
+      const int kn = 2 * kc + t / NC, cn = t % NC;
+      k_ = Tile::template row_frag_at<T>(tK + kn * Tile::kBlk16 + lo.row[cn]);
+      v_ = Tile::template row_frag_at<T>(tV + kn * Tile::kBlk16 + lo.row[cn]);
+    };
+    Frag<T> kf[3], vf[3];
+    row_kv(0, kf[0], vf[0]);
+    row_kv(1, kf[1], vf[1]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       f32x4 sc[QB], dp[QB];
@@ -667,16 +675,13 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int t = h * NC + c;
-        if (t + 1 < 2 * NC) {
-          const int kn = 2 * kc + (t + 1) / NC, cn = (t + 1) % NC;
-          kf[(t + 1) & 1] = Tile::template row_frag_at<T>(tK + kn * Tile::kBlk16 + lo.row[cn]);
-          vf[(t + 1) & 1] = Tile::template row_frag_at<T>(tV + kn * Tile::kBlk16 + lo.row[cn]);
-        }
+        if (t + 2 < NT) row_kv(t + 2, kf[(t + 2) % 3], vf[(t + 2) % 3]);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-          sc[qb] = mma(sc[qb], kf[t & 1], qf[qb][c]);
-          dp[qb] = mma(dp[qb], vf[t & 1], df[qb][c]);
+          sc[qb] = mma(sc[qb], kf[t % 3], qf[qb][c]);
+          dp[qb] = mma(dp[qb], vf[t % 3], df[qb][c]);
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
       const int kb = 2 * kc + h;
 #pragma unroll
@@ -697,18 +702,21 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
                            ds[1][qb][0], ds[1][qb][1], ds[1][qb][2], ds[1][qb][3]};
       dsf[qb] = pack8<T>(v8);
     }
-    // transposed K fragments, also one step ahead
-    Frag<T> kt[2];
+    // transposed K fragments, also two steps ahead
+    Frag<T> kt[3];
     auto tr_k = [&](int db) {
       const char* pa = tK + (2 * kc) * Tile::kBlk16 + lo.tr[db];
       return Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
     };
     kt[0] = tr_k(0);
+    kt[1] = tr_k(1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
-      if (db + 1 < D / 16) kt[(db + 1) & 1] = tr_k(db + 1);
+      if (db + 2 < D / 16) kt[(db + 2) % 3] = tr_k(db + 2);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) dqa[db][qb] = mma(dqa[db][qb], kt[db & 1], dsf[qb]);
+      for (int qb = 0; qb < QB; ++qb) dqa[db][qb] = mma(dqa[db][qb], kt[db % 3], dsf[qb]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -901,30 +909,36 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
                                            const int (&qmax)[KB], const unsigned (&qspan)[KB]) {
   using Tile = SwzTile<D, BQ>;
   constexpr int NS = BQ / 32;  // 32-query subtiles
+  // LDS fragments are read PF MFMA steps ahead of their use; scheduling
+  // fences keep the compiler from moving the reads next to their uses
+  constexpr int PF = 2;
   // S = Q . K^T and dP = dO . V^T of subtile qs (two 16-query blocks)
   // Fragments are read one step ahead of the MFMAs that use them.
   auto scores = [&](int qs, f32x4 (&sc)[2][KB], f32x4 (&dp)[2][KB]) {
-    constexpr int NC = D / 32;
-    Frag<T> qa[2], oa[2];
-    qa[0] = Tile::template row_frag_at<T>(tQ + (2 * qs) * Tile::kBlk16 + lo.row[0]);
-    oa[0] = Tile::template row_frag_at<T>(tO + (2 * qs) * Tile::kBlk16 + lo.row[0]);
+    constexpr int NC = D / 32, NT = 2 * NC;
+    auto row_qo = [&](int t, Frag<T>& q_, Frag<T>& o_) {
+      const int qn = 2 * qs + t / NC, cn = t % NC;
+      q_ = Tile::template row_frag_at<T>(tQ + qn * Tile::kBlk16 + lo.row[cn]);
+      o_ = Tile::template row_frag_at<T>(tO + qn * Tile::kBlk16 + lo.row[cn]);
+    };
+    Frag<T> qa[PF + 1], oa[PF + 1];
+#pragma unroll
+    for (int t = 0; t < PF; ++t) row_qo(t, qa[t], oa[t]);
 #pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) sc[qb2][kb] = dp[qb2][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 2 * NC; ++t) {
+    for (int t = 0; t < NT; ++t) {
       const int qb2 = t / NC, c = t % NC;
-      if (t + 1 < 2 * NC) {
-        const int qn = 2 * qs + (t + 1) / NC, cn = (t + 1) % NC;
-        qa[(t + 1) & 1] = Tile::template row_frag_at<T>(tQ + qn * Tile::kBlk16 + lo.row[cn]);
-        oa[(t + 1) & 1] = Tile::template row_frag_at<T>(tO + qn * Tile::kBlk16 + lo.row[cn]);
-      }
+      if (t + PF < NT) row_qo(t + PF, qa[(t + PF) % (PF + 1)], oa[(t + PF) % (PF + 1)]);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        sc[qb2][kb] = mma(sc[qb2][kb], qa[t & 1], kf[kb][c]);
-        dp[qb2][kb] = mma(dp[qb2][kb], oa[t & 1], vf[kb][c]);
+        sc[qb2][kb] = mma(sc[qb2][kb], qa[t % (PF + 1)], kf[kb][c]);
+        dp[qb2][kb] = mma(dp[qb2][kb], oa[t % (PF + 1)], vf[kb][c]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
   // Each subtile's scores, then its exponentials, in sequence: 160 VGPRs,
@@ -974,19 +988,22 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
                            ds[1][kb][0], ds[1][kb][1], ds[1][kb][2], ds[1][kb][3]};
       const Frag<T> pf = pack8<T>(pv);
       const Frag<T> sf = pack8<T>(sv);
-      Frag<T> ot[2], qt[2];
+      Frag<T> ot[PF + 1], qt[PF + 1];
       auto tr_pair = [&](int db, Frag<T>& o_, Frag<T>& q_) {
         const char* po = tO + (2 * qs) * Tile::kBlk16 + lo.tr[db];
         const char* pq = tQ + (2 * qs) * Tile::kBlk16 + lo.tr[db];
         o_ = Tile::template tr_frag_at<T>(po, po + Tile::kBlk16);
         q_ = Tile::template tr_frag_at<T>(pq, pq + Tile::kBlk16);
       };
-      tr_pair(0, ot[0], qt[0]);
+#pragma unroll
+      for (int db = 0; db < PF; ++db) tr_pair(db, ot[db], qt[db]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int db = 0; db < D / 16; ++db) {
-        if (db + 1 < D / 16) tr_pair(db + 1, ot[(db + 1) & 1], qt[(db + 1) & 1]);
-        dva[db][kb] = mma(dva[db][kb], ot[db & 1], pf);
-        dka[db][kb] = mma(dka[db][kb], qt[db & 1], sf);
+        if (db + PF < D / 16) tr_pair(db + PF, ot[(db + PF) % (PF + 1)], qt[(db + PF) % (PF + 1)]);
+        dva[db][kb] = mma(dva[db][kb], ot[db % (PF + 1)], pf);
+        dka[db][kb] = mma(dka[db][kb], qt[db % (PF + 1)], sf);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
