@@ -175,6 +175,39 @@ def load_library():
         return lib
 
 
+_TORCH_LIB_NAME = "libcra_torch.so"
+_op_state = {"tried": False, "op": None, "error": None}
+
+
+def torch_op_path() -> str:
+    return os.environ.get("CRA_TORCH_LIBRARY",
+                          os.path.join(os.path.dirname(os.path.abspath(__file__)), _TORCH_LIB_NAME))
+
+
+def attention_op():
+    """``torch.ops.cra.attention`` bound to the loaded libcra_hip.so, or None
+    when libcra_torch.so is absent (then the Python autograd Function serves
+    every call; both launch the same kernels through the same C ABI)."""
+    if _op_state["tried"]:
+        return _op_state["op"]
+    load_library()  # raises without the HIP library (takes _lock itself)
+    with _lock:
+        if not _op_state["tried"]:
+            lib_path = library_path()
+            path = torch_op_path()
+            if os.path.exists(path):
+                try:
+                    torch.ops.load_library(path)
+                    torch.ops.cra.bind(lib_path)
+                    _op_state["op"] = torch.ops.cra.attention
+                except (OSError, RuntimeError) as e:
+                    _op_state["error"] = f"{path}: {e}"
+            else:
+                _op_state["error"] = f"{path} not found"
+            _op_state["tried"] = True
+    return _op_state["op"]
+
+
 def _raise(code: int, func: str):
     lib = load_library()
     msg = (lib.cra_last_error() or b"").decode() or lib.cra_strerror(code).decode()

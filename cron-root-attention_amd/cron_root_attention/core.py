@@ -269,8 +269,39 @@ def cron_root_attention_v14(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
             return CronRootAttentionCPUFunction.apply(q, k, v)
         return _cpu_forward(q, k, v)
+    if relay_log_scale is None:
+        op = _native.attention_op()
+        if op is not None:
+            plan = _op_plan(q, k, v, use_persistent, kv_groups, relay_top_k)
+            if plan is not None:
+                return op(q, k, v, *plan)
     return CronRootAttentionV14Function.apply(q, k, v, use_persistent, kv_groups,
                                               relay_log_scale, relay_top_k)
+
+
+_OP_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _op_plan(q, k, v, use_persistent, kv_groups, relay_top_k):
+    """(window, relay, top_k, scale) when the call can go to the C++ operator
+    ``torch.ops.cra.attention`` (the Function's plan and launches, bit for
+    bit, without its Python host cost; it copies layouts the kernels cannot
+    take, as the Function does): q, k, v on one GPU, head dim 32/64/128, the
+    tiled forward. None sends the call to the Python Function, which also
+    raises the reference's errors for invalid arguments."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        return None
+    B, Hq, S, D = q.shape
+    if (D not in _SUPPORTED_D or S < 1 or B < 1 or k.shape != v.shape
+            or k.shape[0] != B or k.shape[2] != S or k.shape[3] != D
+            or kv_groups < 1 or k.shape[1] * kv_groups != Hq
+            or not (q.dtype == k.dtype == v.dtype) or q.dtype not in _OP_DTYPES
+            or q.device.type != "cuda" or not (q.device == k.device == v.device)):
+        return None
+    relay = S > RELAY_THRESHOLD
+    if (use_persistent and not relay) or (relay and not 1 <= relay_top_k <= 4):
+        return None
+    return window_size(S), relay, int(relay_top_k), 1.0 / math.sqrt(D)
 
 
 def _attention_with_plan(q, k, v, window: int, relay: bool, kv_groups: int = 1,
