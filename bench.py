@@ -578,7 +578,7 @@ def run_crossover(args):
     dev = torch.device("cuda", 0)
     shapes = ((2, 32, 128, torch.bfloat16), (1, 16, 128, torch.float16),
               (1, 8, 64, torch.float16), (1, 12, 64, torch.float16))
-    seqs = (256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384)
+    seqs = (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384)
     for (B, H, D, dtype) in shapes:
         points = []
         backend = None

@@ -1,17 +1,17 @@
 """SDPA / sqrt(N) dispatch by sequence length (reference hybrid.py:1-124).
 
 The reference's crossover (1536 tokens, hybrid.py:22) was measured on an RTX
-5070 Ti.  Here the crossover is a gfx950 table measured on one MI355X with
+5070 Ti.  Here the crossover is a gfx950 table measured on MI355X boxes with
 ``bench.py --crossover`` against ROCm's fused (flash) SDPA, causal, for
 forward and forward+backward separately: ``CROSSOVER_GFX950``.  Below a few
-thousand tokens the sqrt(N) op costs its launch floor (about 37 us forward,
-190-210 us forward+backward) while SDPA grows with B*H*S^2, so the crossover
-falls as B*H grows; the table keeps one row per measured B*H.
-The training floor is host-bound and moves with the host (the sqrt(N) op's
-forward+backward floor measured 0.10 and 0.18 ms on two boxes at B=1), so
-each row is the larger crossover of two boxes.  ``_SDPA_THRESHOLD`` is the
-forward+backward crossover at D=128 for B*H=16, the role of the reference's
-constant.  Both entry points default to
+thousand tokens the sqrt(N) op costs its launch floor (about 15 us forward
+and 80-110 us forward+backward through the C++ operator) while SDPA's floor
+is 25 us and 110-130 us and grows with B*H*S^2; on two boxes the sqrt(N) op
+was the faster at every swept S from 64 up, for every BASELINE shape and both
+modes, so every row is 64, the smallest swept S.  The table keeps its shape
+(mode, head dim, B*H) for re-measurement on other hosts.
+``_SDPA_THRESHOLD`` is the forward+backward crossover at D=128 for B*H=16, the
+role of the reference's constant.  Both entry points default to
 ``threshold=None``, which looks the crossover up in the table for the call's
 head dim, B*H and grad mode; an integer threshold behaves as the reference's
 (S >= threshold runs the sqrt(N) op).
@@ -27,18 +27,17 @@ import torch.nn.functional as F
 from .core import cron_root_attention_v14
 
 # (mode, head_dim, smallest B*H the row applies to) -> smallest swept S from
-# which the sqrt(N) op beats SDPA at every larger swept S. Sweep: S in
-# {256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384};
-# shapes (B, H, D, dtype) = (1, 16, 128, fp16), (2, 32, 128, bf16),
-# (1, 8, 64, fp16), (1, 12, 64, fp16).
+# which the sqrt(N) op beats SDPA at every larger swept S, on both boxes.
+# Sweep: S in {64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096,
+# 6144, 8192, 16384}; shapes (B, H, D, dtype) = (1, 16, 128, fp16),
+# (2, 32, 128, bf16), (1, 8, 64, fp16), (1, 12, 64, fp16).
 CROSSOVER_GFX950 = {
-    ("fwd", 128, 1): 768,      # B=1 H=16 fp16 (fwd 0.036 vs 0.044 ms at S=768)
-    ("fwd", 128, 64): 512,     # B=2 H=32 bf16 (0.039 vs 0.041 ms at S=512)
-    ("train", 128, 1): 1024,   # B=1 H=16 fp16 (0.18 vs 0.20 ms at S=1024 on the slower host;
-                               # 512 on the faster one)
-    ("train", 128, 64): 512,   # B=2 H=32 bf16 (0.189 vs 0.193 ms at S=512)
-    ("fwd", 64, 1): 1536,      # B=1 H=8 and H=12 fp16
-    ("train", 64, 1): 2048,    # B=1 H=8 and H=12 fp16 (768 on the faster host)
+    ("fwd", 128, 1): 64,       # B=1 H=16 fp16: 0.015 vs 0.025 ms at S=64
+    ("fwd", 128, 64): 64,      # B=2 H=32 bf16: 0.020 vs 0.026 ms
+    ("train", 128, 1): 64,     # B=1 H=16 fp16: 0.091 vs 0.118 ms
+    ("train", 128, 64): 64,    # B=2 H=32 bf16: 0.097 vs 0.131 ms
+    ("fwd", 64, 1): 64,        # B=1 H=8 and H=12 fp16: 0.015 vs 0.025 ms
+    ("train", 64, 1): 64,      # B=1 H=8 and H=12 fp16: 0.090 vs 0.116 ms
 }
 _SDPA_THRESHOLD = CROSSOVER_GFX950[("train", 128, 1)]
 
