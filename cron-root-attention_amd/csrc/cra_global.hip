@@ -7,8 +7,9 @@
 // first row (core.py:2668-2669). Unlike the reference, which walks the W rows
 // of a block one at a time in a single program, one 256-thread workgroup scans
 // a block with D/8 lanes per row; every row group keeps its own sorted top-4
-// and the lists are merged with the same (norm desc, row asc) order, which
-// yields the same selection as the sequential scan.
+// and one wave merges the lists with the same (norm desc, row asc) order (a
+// wave-wide maximum per pick), which yields the same selection as the
+// sequential scan.
 //
 // The squared norm of a row is summed in one fixed order so a CPU check can
 // reproduce it bit for bit: each lane sums the squares of its 8 consecutive
@@ -22,6 +23,20 @@ namespace cra {
 namespace {
 
 constexpr float kSentinel = -1e38f;  // below any squared norm
+
+// 64-bit rank of a candidate: larger key = larger norm, then smaller row.
+// The float's bits are mapped to an unsigned order-preserving form (sign bit
+// set for x >= 0, all bits flipped for x < 0); every key is above 0.
+__device__ __forceinline__ uint64_t rank_key(float norm, int row) {
+  const uint32_t b = __float_as_uint(norm);
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(~(uint32_t)row);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int off) {
+  const uint32_t lo = __shfl_xor((uint32_t)x, off), hi = __shfl_xor((uint32_t)(x >> 32), off);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
@@ -100,19 +115,42 @@ __global__ __launch_bounds__(256) void build_global_kernel(GlobalArgs a) {
       }
     }
     __syncthreads();
-    if (tid == 0) {
-      // A taken candidate is parked at -inf, below the sentinel of unset slots.
-      for (int j = 0; j < a.top_k; ++j) {
-        int best = 0;
-        for (int c = 1; c < kNRG * 4; ++c) {
-          if (s_norm[c] > s_norm[best] || (s_norm[c] == s_norm[best] && s_idx[c] < s_idx[best]))
-            best = c;
-        }
-        s_sel[j] = row0 + s_idx[best];
-        s_norm[best] = -__builtin_huge_valf();
+    if (tid < 64) {
+      // Wave 0 merges the row groups' lists: each candidate becomes a 64-bit
+      // key ordered as (norm desc, row asc) -- the float's order-preserving
+      // bits above the complemented row -- and every pick is a wave-wide
+      // maximum. A picked candidate's key becomes 0, below every candidate
+      // (the sentinel of an unset slot included); of equal keys (unset slots
+      // of one group list) only one is taken per pick.
+      constexpr int kNC = kNRG * 4, kPer = (kNC + 63) / 64;
+      uint64_t key[kPer];
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int c = tid + 64 * q;
+        key[q] = c < kNC ? rank_key(s_norm[c], s_idx[c]) : 0ull;
       }
-      int32_t* src = a.src + ((int64_t)bh * a.NB + dc.bofs + r) * a.top_k;
-      for (int j = 0; j < a.top_k; ++j) src[j] = s_sel[j];
+      int mine = 0;  // lane j keeps pick j
+      for (int j = 0; j < a.top_k; ++j) {
+        uint64_t m = key[0];
+#pragma unroll
+        for (int q = 1; q < kPer; ++q) m = key[q] > m ? key[q] : m;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+          const uint64_t o = shfl_xor_u64(m, off);
+          m = o > m ? o : m;
+        }
+        // the lowest lane holding the maximum takes one copy of it
+        int hit = -1;
+#pragma unroll
+        for (int q = kPer - 1; q >= 0; --q) hit = key[q] == m ? q : hit;
+        const uint64_t holders = __ballot(hit >= 0);
+        if (tid == __builtin_ctzll(holders)) key[hit] = 0ull;
+        if (tid == j) mine = row0 + (int)~(uint32_t)m;
+      }
+      if (tid < a.top_k) {
+        s_sel[tid] = mine;
+        a.src[((int64_t)bh * a.NB + dc.bofs + r) * a.top_k + tid] = mine;
+      }
     }
     __syncthreads();
   }
