@@ -639,14 +639,15 @@ __device__ __forceinline__ LaneOffs<D> lane_offs(int lane) {
 }
 
 // Query-centric dQ for QB blocks of 16 queries per wave against one BN-key
-// tile, in 32-key halves: S = K . Q^T and dP = V . dO^T (key on rows),
-// dS = P * (dP - Delta), dQ^T += K^T . dS^T.
+// tile, in 32-key halves: S = K . Q^T and dP - Delta = V . dO^T - Delta (key
+// on rows; the products accumulate onto -Delta, so no subtraction per
+// element), dS = P * (dP - Delta), dQ^T += K^T . dS^T.
 template <typename T, int D, int QB, int BN, bool MASK>
 __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const LaneOffs<D>& lo,
                                          const Frag<T> (&qf)[QB][D / 32],
                                          const Frag<T> (&df)[QB][D / 32],
                                          f32x4 (&dqa)[D / 16][QB], const float (&lse2)[QB],
-                                         const float (&dl)[QB], float c2, int g,
+                                         const float (&ndl)[QB], float c2, int g,
                                          const TileMask& mk, bool half0, bool half1) {
   using Tile = SwzTile<D, BN>;
   constexpr int NC = D / 32;
@@ -671,7 +672,10 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
     for (int h = 0; h < 2; ++h) {
       f32x4 sc[QB], dp[QB];
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) sc[qb] = dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int qb = 0; qb < QB; ++qb) {
+        sc[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[qb] = f32x4{ndl[qb], ndl[qb], ndl[qb], ndl[qb]};
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int t = h * NC + c;
@@ -691,7 +695,7 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
         for (int qb = 0; qb < QB; ++qb) {
           float x = fmaf(sc[qb][r], c2, -lse2[qb]);
           if (MASK && !mk.ok(ko, qb)) x = -__builtin_huge_valf();
-          ds[h][qb][r] = __builtin_amdgcn_exp2f(x) * (dp[qb][r] - dl[qb]);
+          ds[h][qb][r] = __builtin_amdgcn_exp2f(x) * dp[qb][r];
         }
       }
     }
@@ -792,10 +796,11 @@ void dq2_kernel(BwdArgs a) {
   const LaneOffs<D> lo = lane_offs<D>(lane);
   Frag<T> qf[QB][D / 32], df[QB][D / 32];
   int qi[QB];
-  float lse2[QB], dl[QB];
+  float lse2[QB], ndl[QB];
   // Delta = rowsum(O * dO) of this wave's queries, computed here and stored
-  // for the dK/dV kernels: lane (l16, g) sums its 32 columns, then the four
-  // lanes of a query add theirs in a fixed order.
+  // negated (-Delta, the initial value of the dP accumulators) for the dK/dV
+  // kernels: lane (l16, g) sums its 32 columns, then the four lanes of a
+  // query add theirs in a fixed order.
   const T* opp = static_cast<const T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
   // All of the wave's Q, dO and O fragments are loaded before any is used
   // (rows past the document read its last row: those queries' results are
@@ -828,8 +833,8 @@ void dq2_kernel(BwdArgs a) {
     }
     od += __shfl_xor(od, 16);
     od += __shfl_xor(od, 32);
-    dl[qb] = od;
-    if (ok && g == 0) delta[qi[qb]] = od;
+    ndl[qb] = -od;
+    if (ok && g == 0) delta[qi[qb]] = -od;
   }
   const float c2 = a.scale * kLog2e;
   f32x4 dqa[D / 16][QB];
@@ -874,9 +879,9 @@ void dq2_kernel(BwdArgs a) {
       const int vis_hi = loc ? q_last - ts : wg_hi - 1 - ts;
       const bool half0 = vis_lo <= 31, half1 = vis_hi >= 32;
       if (full)
-        dq2_tile<T, D, QB, BN, false>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, true, true);
+        dq2_tile<T, D, QB, BN, false>(tK, tV, lo, qf, df, dqa, lse2, ndl, c2, g, mk, true, true);
       else
-        dq2_tile<T, D, QB, BN, true>(tK, tV, lo, qf, df, dqa, lse2, dl, c2, g, mk, half0, half1);
+        dq2_tile<T, D, QB, BN, true>(tK, tV, lo, qf, df, dqa, lse2, ndl, c2, g, mk, half0, half1);
     }
   };
   for (int it = 0; it < ntot; it += 2) {
@@ -912,8 +917,8 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
   // LDS fragments are read PF MFMA steps ahead of their use; scheduling
   // fences keep the compiler from moving the reads next to their uses
   constexpr int PF = 2;
-  // S = Q . K^T and dP = dO . V^T of subtile qs (two 16-query blocks)
-  // Fragments are read one step ahead of the MFMAs that use them.
+  // S = Q . K^T and dP - Delta = dO . V^T - Delta of subtile qs (two
+  // 16-query blocks; sDl holds -Delta, the dP accumulators' initial value)
   auto scores = [&](int qs, f32x4 (&sc)[2][KB], f32x4 (&dp)[2][KB]) {
     constexpr int NC = D / 32, NT = 2 * NC;
     auto row_qo = [&](int t, Frag<T>& q_, Frag<T>& o_) {
@@ -925,9 +930,14 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
 #pragma unroll
     for (int t = 0; t < PF; ++t) row_qo(t, qa[t], oa[t]);
 #pragma unroll
-    for (int qb2 = 0; qb2 < 2; ++qb2)
+    for (int qb2 = 0; qb2 < 2; ++qb2) {
+      const f32x4 ndq = *reinterpret_cast<const f32x4*>(sDl + 16 * (2 * qs + qb2) + 4 * g);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) sc[qb2][kb] = dp[qb2][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < KB; ++kb) {
+        sc[qb2][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[qb2][kb] = ndq;
+      }
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -963,7 +973,6 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
     for (int qb2 = 0; qb2 < 2; ++qb2) {
       const int qblk = 2 * qs + qb2;
       const f32x4 lq = *reinterpret_cast<const f32x4*>(sL + 16 * qblk + 4 * g) * kLog2e;
-      const f32x4 dq = *reinterpret_cast<const f32x4*>(sDl + 16 * qblk + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
@@ -976,7 +985,7 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
             if (out) x = -__builtin_huge_valf();
           }
           p[qb2][kb][r] = __builtin_amdgcn_exp2f(x);
-          ds[qb2][kb][r] = p[qb2][kb][r] * (dp[qb2][kb][r] - dq[r]);
+          ds[qb2][kb][r] = p[qb2][kb][r] * dp[qb2][kb][r];
         }
       }
     }
