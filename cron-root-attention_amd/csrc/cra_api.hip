@@ -319,11 +319,13 @@ int bwd_impl(const cra_problem* p, const Plan& pl, cra_tensor q, cra_tensor k, c
   a.G = pl.G;
   a.scale = p->scale;
   a.nchunk = nchunk;
-  // workspace carve-up: delta [B*Hq*S] fp32, then the global-row partials
+  // workspace carve-up: delta and nlse2 [B*Hq*S] fp32 each, then the
+  // global-row partials
   char* ws = static_cast<char*>(workspace);
   const size_t delta_bytes = (((size_t)p->B * p->H_q * p->S * 4) + 255) / 256 * 256;
   a.delta = reinterpret_cast<float*>(ws);
-  a.gpart = reinterpret_cast<float*>(ws + delta_bytes);
+  a.nlse2 = reinterpret_cast<float*>(ws + delta_bytes);
+  a.gpart = reinterpret_cast<float*>(ws + 2 * delta_bytes);
   a.dalpha = dalpha;
   for (int g = 0; g < num_groups(pl); ++g) {
     a.group = g;

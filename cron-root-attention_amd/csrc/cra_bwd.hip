@@ -756,6 +756,7 @@ void dq2_kernel(BwdArgs a) {
   const T* vp = static_cast<const T*>(a.v) + b * a.vsb + hk * a.vsh + (int64_t)dc.off * a.vss;
   const float* lse = a.lse + (int64_t)bh * a.S + dc.off;
   float* delta = a.delta + (int64_t)bh * a.S + dc.off;
+  float* nlse2 = a.nlse2 + (int64_t)bh * a.S + dc.off;
   const int64_t gbase = ((int64_t)(b * a.Hkv + hk) * a.G + dc.gofs) * D;
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
@@ -799,8 +800,9 @@ void dq2_kernel(BwdArgs a) {
   float lse2[QB], ndl[QB];
   // Delta = rowsum(O * dO) of this wave's queries, computed here and stored
   // negated (-Delta, the initial value of the dP accumulators) for the dK/dV
-  // kernels: lane (l16, g) sums its 32 columns, then the four lanes of a
-  // query add theirs in a fixed order.
+  // kernels, with -lse * log2(e) (their exponent's offset): lane (l16, g)
+  // sums its 32 columns, then the four lanes of a query add theirs in a
+  // fixed order.
   const T* opp = static_cast<const T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
   // All of the wave's Q, dO and O fragments are loaded before any is used
   // (rows past the document read its last row: those queries' results are
@@ -834,7 +836,10 @@ void dq2_kernel(BwdArgs a) {
     od += __shfl_xor(od, 16);
     od += __shfl_xor(od, 32);
     ndl[qb] = -od;
-    if (ok && g == 0) delta[qi[qb]] = -od;
+    if (ok && g == 0) {
+      delta[qi[qb]] = -od;
+      nlse2[qi[qb]] = -lse2[qb];
+    }
   }
   const float c2 = a.scale * kLog2e;
   f32x4 dqa[D / 16][QB];
@@ -901,7 +906,8 @@ void dq2_kernel(BwdArgs a) {
 
 // Key-centric dK/dV: each wave owns KB blocks of 16 key rows (rows of k/v,
 // or packed global rows with GLOB), B operands in registers; query tiles of
-// BQ rows of Q and dO stream through LDS with their LSE and Delta. A key row
+// BQ rows of Q and dO stream through LDS with their -lse * log2(e) (sL) and
+// -Delta (sDl), both written by dq2_kernel. A key row
 // j sees the queries [j, j+W-1] (local) or [first_query(j), S) (global rows),
 // so every mask is a per-key interval.
 template <typename T, int D, int KB, int BQ, bool MASK, bool LOC>
@@ -972,12 +978,12 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
 #pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2) {
       const int qblk = 2 * qs + qb2;
-      const f32x4 lq = *reinterpret_cast<const f32x4*>(sL + 16 * qblk + 4 * g) * kLog2e;
+      const f32x4 nlq = *reinterpret_cast<const f32x4*>(sL + 16 * qblk + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          float x = fmaf(sc[qb2][kb][r], c2, -lq[r]);
+          float x = fmaf(sc[qb2][kb][r], c2, nlq[r]);
           if (MASK) {
             const bool out = LOC ? (unsigned)(16 * qblk + r - q0[kb]) > qspan[kb]
                                  : (ts + 16 * qblk + 4 * g + r < qmin[kb] ||
@@ -1029,10 +1035,10 @@ void dkdv2_kernel(BwdArgs a) {
   constexpr int kKW = 16 * KB, kBK = NW * kKW, kBQ = BQ;
   static_assert(BQ == 32 || BQ == 64 || BQ == 128, "query tile rows");
   // Two pipeline stages as separate LDS objects (see fwd2_kernel): Q and dO
-  // rows, and their LSE and Delta.
+  // rows, and their -lse * log2(e) and -Delta.
   __shared__ __attribute__((aligned(1024))) char stage0[2][Tile::kBytes];
   __shared__ __attribute__((aligned(1024))) char stage1[2][Tile::kBytes];
-  __shared__ __attribute__((aligned(16))) float sld0[2][kBQ];  // [lse, delta][q]
+  __shared__ __attribute__((aligned(16))) float sld0[2][kBQ];  // [-lse log2 e, -delta][q]
   __shared__ __attribute__((aligned(16))) float sld1[2][kBQ];
 
   const int tid = threadIdx.x;
@@ -1155,7 +1161,7 @@ void dkdv2_kernel(BwdArgs a) {
     r.o = make_rsrc(
         static_cast<const T*>(a.dout) + b * a.dosb + hq * a.dosh + (int64_t)dc.off * a.doss,
         (uint32_t)((q_hi - 1) * obytes + D * 2));
-    r.l = make_rsrc(a.lse + bh * a.S + dc.off, (uint32_t)(S * 4));
+    r.l = make_rsrc(a.nlse2 + bh * a.S + dc.off, (uint32_t)(S * 4));
     r.d = make_rsrc(a.delta + bh * a.S + dc.off, (uint32_t)(S * 4));
     return r;
   };
@@ -1400,9 +1406,10 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
 }
 
 size_t bwd_workspace_layout(int D, int B, int Hq, int Hkv, int S, int64_t G, int nchunk) {
+  // Delta and -lse * log2(e) per query, then the chunk partials
   const size_t delta = (((size_t)B * Hq * S * 4) + 255) / 256 * 256;
   const size_t part = (size_t)nchunk * B * Hkv * G * 2 * D * 4;
-  return delta + part;
+  return 2 * delta + part;
 }
 
 bool bwd_tile_config(int dtype, int D, int out[9]) {

@@ -82,7 +82,8 @@ struct BwdArgs {
   void* dq;
   void* dk;
   void* dv;
-  float* delta;    // [B, Hq, S] rowsum(o * do)
+  float* delta;    // [B, Hq, S] rowsum(o * do); 2-byte path: stored negated
+  float* nlse2;    // [B, Hq, S] 2-byte path: -lse * log2(e)
   float* gpart;    // [nchunk, B, Hkv, G, 2, D] fp32 partial dK/dV of the global rows
   float* dalpha;   // [Hkv] or null
   int64_t qsb, qsh, qss, ksb, ksh, kss, vsb, vsh, vss, osb, osh, oss;
