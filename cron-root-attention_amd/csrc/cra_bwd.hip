@@ -1291,7 +1291,7 @@ void dkdv2_kernel(BwdArgs a) {
 // backward, 4 waves 3% slower than 8); the local
 // kernel 4 waves (64 rows: its band of queries, 64 + W - 1, wastes fewer
 // pairs than with 128 rows; measured 7% faster). dQ workgroups: 4 waves of
-// 32 queries, 64-key tiles, 2 waves per SIMD at 249 VGPRs (each K/V
+// 32 queries, 64-key tiles, 2 waves per SIMD at 246 VGPRs (each K/V
 // fragment read from LDS serves two query blocks). 16 queries per wave
 // lose that reuse: 8 waves measured 27% slower, and with 32-key tiles at
 // 3 or 4 waves per SIMD still 5-10% slower backward at D = 128.

@@ -255,6 +255,14 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
 // O and LSE are exact for any reference max). The normaliser l sums the
 // rounded P that the P.V MFMAs use.
 // ---------------------------------------------------------------------------
+// MFMA steps by which the forward's LDS operand reads run ahead of their use
+// (K row fragments and transposed V fragments). Three measured 0.6% faster
+// than two and four no better than two (D = 128: 242, 238 and 246 VGPRs, 2
+// waves per SIMD either way; D = 64 stays at 168, 3 waves per SIMD).
+#ifndef CRA_FWD_PF
+#define CRA_FWD_PF 3
+#endif
+
 template <int D>
 struct Fwd2Lane {
   int k[D / 32];   // K row fragment, chunk 4c + g, row lane%16
@@ -267,28 +275,29 @@ __device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& l
                                             f32x4 (&s)[2][2]) {
   using Tile = SwzTile<D, BN>;
   constexpr int NC = D / 32, NK = 2 * NC;
-  // K fragments are read two steps ahead of the MFMAs that use them; fences
+  // K fragments are read CRA_FWD_PF steps ahead of the MFMAs that use them; fences
   // keep the compiler from moving the reads next to their uses
   auto k_frag = [&](int t) {
     return Tile::template row_frag_at<T>(tK + (2 * kc + t / NC) * Tile::kBlk16 + lo.k[t % NC]);
   };
-  Frag<T> kf[3];
-  kf[0] = k_frag(0);
-  kf[1] = k_frag(1);
+  constexpr int PF = CRA_FWD_PF < NK ? CRA_FWD_PF : NK;
+  Frag<T> kf[PF + 1];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) kf[t] = k_frag(t);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < NK; ++t) {
-    if (t + 2 < NK) kf[(t + 2) % 3] = k_frag(t + 2);
+    if (t + PF < NK) kf[(t + PF) % (PF + 1)] = k_frag(t + PF);
     const int h = t / NC, c = t % NC;
     if (c == 0) s[h][0] = s[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    s[h][0] = mma(s[h][0], kf[t % 3], qf[0][c]);
-    s[h][1] = mma(s[h][1], kf[t % 3], qf[1][c]);
+    s[h][0] = mma(s[h][0], kf[t % (PF + 1)], qf[0][c]);
+    s[h][1] = mma(s[h][1], kf[t % (PF + 1)], qf[1][c]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-// O^T += V^T . P^T for 32-key half kh: transposed V fragments read one step
-// ahead of the MFMAs that use them.
+// O^T += V^T . P^T for 32-key half kh: transposed V fragments read
+// CRA_FWD_PF steps ahead of the MFMAs that use them.
 template <typename T, int D, int BN>
 __device__ __forceinline__ void pv_half(const char* tV, int kh, const Fwd2Lane<D>& lo,
                                         const Frag<T> (&pf)[2], f32x4 (&acc)[D / 16][2]) {
@@ -298,15 +307,16 @@ __device__ __forceinline__ void pv_half(const char* tV, int kh, const Fwd2Lane<D
     const char* pa = tV + (2 * kh) * Tile::kBlk16 + lo.v[db];
     return Tile::template tr_frag_at<T>(pa, pa + Tile::kBlk16);
   };
-  Frag<T> vt[3];
-  vt[0] = tr_v(0);
-  vt[1] = tr_v(1);
+  constexpr int PF = CRA_FWD_PF < NDB ? CRA_FWD_PF : NDB;
+  Frag<T> vt[PF + 1];
+#pragma unroll
+  for (int db = 0; db < PF; ++db) vt[db] = tr_v(db);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int db = 0; db < NDB; ++db) {
-    if (db + 2 < NDB) vt[(db + 2) % 3] = tr_v(db + 2);
-    acc[db][0] = mma(acc[db][0], vt[db % 3], pf[0]);
-    acc[db][1] = mma(acc[db][1], vt[db % 3], pf[1]);
+    if (db + PF < NDB) vt[(db + PF) % (PF + 1)] = tr_v(db + PF);
+    acc[db][0] = mma(acc[db][0], vt[db % (PF + 1)], pf[0]);
+    acc[db][1] = mma(acc[db][1], vt[db % (PF + 1)], pf[1]);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
