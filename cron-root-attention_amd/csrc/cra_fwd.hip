@@ -276,9 +276,12 @@ __device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& l
   using Tile = SwzTile<D, BN>;
   constexpr int NC = D / 32, NK = 2 * NC;
   // K fragments are read CRA_FWD_PF steps ahead of the MFMAs that use them; fences
-  // keep the compiler from moving the reads next to their uses
+  // keep the compiler from moving the reads next to their uses. Step t takes
+  // key block t % 2 and D-chunk t / 2, so the four accumulators alternate and
+  // each MFMA's accumulator was last written four MFMAs earlier (key block
+  // major, two apart, measured 0.5% slower).
   auto k_frag = [&](int t) {
-    return Tile::template row_frag_at<T>(tK + (2 * kc + t / NC) * Tile::kBlk16 + lo.k[t % NC]);
+    return Tile::template row_frag_at<T>(tK + (2 * kc + t % 2) * Tile::kBlk16 + lo.k[t / 2]);
   };
   constexpr int PF = CRA_FWD_PF < NK ? CRA_FWD_PF : NK;
   Frag<T> kf[PF + 1];
@@ -288,7 +291,7 @@ __device__ __forceinline__ void tile_scores(const char* tK, const Fwd2Lane<D>& l
 #pragma unroll
   for (int t = 0; t < NK; ++t) {
     if (t + PF < NK) kf[(t + PF) % (PF + 1)] = k_frag(t + PF);
-    const int h = t / NC, c = t % NC;
+    const int h = t % 2, c = t / 2;
     if (c == 0) s[h][0] = s[h][1] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[h][0] = mma(s[h][0], kf[t % (PF + 1)], qf[0][c]);
     s[h][1] = mma(s[h][1], kf[t % (PF + 1)], qf[1][c]);
