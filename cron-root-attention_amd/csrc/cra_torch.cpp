@@ -15,6 +15,7 @@
 // very library the Python binding loaded.
 #include <dlfcn.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -38,9 +39,11 @@ struct Api {
   decltype(&cra_abi_version) abi_version = nullptr;
 };
 
+// Written once under g_mu by bind(); g_bound is published last (release) and
+// read with acquire, so a reader that sees it set sees the whole table.
 std::mutex g_mu;
 Api g_api;
-bool g_bound = false;
+std::atomic<bool> g_bound{false};
 
 template <typename F>
 void resolve(void* h, const std::string& path, const char* name, F& out) {
@@ -64,12 +67,18 @@ void bind(std::string path) {
   resolve(h, path, "cra_abi_version", api.abi_version);
   TORCH_CHECK(api.abi_version() == CRA_ABI_VERSION, path, ": ABI ", api.abi_version(),
               " != ", CRA_ABI_VERSION);
+  if (g_bound.load(std::memory_order_acquire)) {
+    // already bound (a second bind is a no-op unless it names another library)
+    TORCH_CHECK(api.fwd == g_api.fwd, "cra::bind: already bound to another library");
+    return;
+  }
   g_api = api;
-  g_bound = true;
+  g_bound.store(true, std::memory_order_release);
 }
 
 const Api& api() {
-  TORCH_CHECK(g_bound, "cra::attention: library not bound (call torch.ops.cra.bind first)");
+  TORCH_CHECK(g_bound.load(std::memory_order_acquire),
+              "cra::attention: library not bound (call torch.ops.cra.bind first)");
   return g_api;
 }
 

@@ -24,6 +24,18 @@ def test_operator_rejects_a_missing_library():
     assert _native.attention_op() is not None
 
 
+def test_operator_binds_once(tmp_path):
+    """Binding the library it is bound to again is a no-op; a different copy of
+    the library is refused (a call in flight must not see the table change)."""
+    assert _native.attention_op() is not None
+    torch.ops.cra.bind(_native.library_path())
+    other = tmp_path / "libcra_hip_copy.so"
+    other.write_bytes(open(_native.library_path(), "rb").read())
+    with pytest.raises(RuntimeError, match="already bound"):
+        torch.ops.cra.bind(str(other))
+    assert _native.attention_op() is not None
+
+
 def _meta(shape, dtype=torch.float16, strides=None):
     # a tensor on the meta device stands in for a GPU tensor's shape/layout
     t = torch.empty(shape, dtype=dtype, device="meta")
