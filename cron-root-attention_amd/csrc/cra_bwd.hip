@@ -1380,24 +1380,34 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
 
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
                            const int* W, const int* rpb, int64_t G, int* nchunk) {
-  // About 3072 tiles of 128 global rows (2112 workgroups of the global-row
-  // kernel's 192 rows at the shape below), per document and (b, kv head):
-  // each document's query range cut into the same number of chunks
-  // (multiples of 64 queries). The global-row kernel
-  // runs one workgroup per CU, so its chunks are long jobs and the last
-  // round leaves CUs idle; more chunks shorten that tail at the cost of
-  // more partial sums (written once, reduced once by gsum_kernel). At B=1
-  // H=16 D=128 S=131072 that is 22 chunks; 15 and 29 measured 0.8% and
-  // 0.1% slower backward.
-  int64_t gtiles = 0;
+  // Query chunks of the global-row kernel: each document's query range is
+  // cut into the same number of chunks (multiples of 64 queries), one
+  // workgroup per (row tile, chunk). More chunks balance the uneven
+  // workgroups better (a late row tile sees only the last queries) and
+  // shorten the last round; each chunk costs a partial dK/dV of its rows,
+  // written once and summed once by gsum_kernel. Measured on gfx950 over
+  // 1-48 chunks (training step, 2 sweeps): the best counts fill the kernel's
+  // resident slots about 1.5 times over (256 CUs, one 12-wave workgroup per
+  // CU at D = 128, two 8-wave ones below) until chunks would exceed about
+  // 6144 queries, from which on 6144-query chunks keep the balance:
+  //   B=1 H=16 D=128 S=131072: 22 chunks (16 and 32 within 0.6%)
+  //   B=1 H=12 D=64 S=8192 / 32768 / 131072: 22 / 13 / 22 chunks
+  //   B=2 H=32 D=128 S=4096: 6 (the previous rule's 16 was 12% slower)
+  //   B=1 H=8 D=64 S=16384: 32 (64 was 10% slower)
+  constexpr int kCUs = 256;
+  const int rows = D == 128 ? 16 * kDkdvGlobWaves<128> * kDkdvKB : 16 * kDkdvGlobWaves<64> * kDkdvKB;
+  const int slots = kCUs * (D == 128 ? 1 : 2);
+  int64_t row_tiles = 0;
   int max_len = 1;
   for (int d = 0; d < n; ++d) {
     const int64_t g = (int64_t)(len[d] + W[d] - 1) / W[d] * rpb[d];
-    gtiles += (g + 127) / 128;
+    row_tiles += (g + rows - 1) / rows;
     if (len[d] > max_len) max_len = len[d];
   }
-  const int64_t base = gtiles * B * Hkv;
-  int64_t nc = (3072 + base - 1) / base;
+  const int64_t base = row_tiles * B * Hkv;
+  int64_t nc = (3 * slots + 2 * base - 1) / (2 * base);  // 1.5 rounds of workgroups
+  const int64_t by_len = (max_len + 6143) / 6144;
+  if (nc < by_len) nc = by_len;
   const int64_t max_nc = (max_len + 255) / 256;
   if (nc > max_nc) nc = max_nc;
   if (nc < 1) nc = 1;
