@@ -23,6 +23,8 @@ Other modes:
                        the hybrid dispatcher with SDPA beside it), one JSON line
                        per point
   --crossover          sweep S against torch's SDPA (forward and fwd+bwd)
+  --sdpa-dense         torch's fused SDPA on dense causal attention at long S,
+                       as TFLOP/s and fraction of the fp16 MFMA peak (context)
   --profile-workload   short fixed workload for rocprofv3 --pmc passes
   --counter-summary D  markdown summary of rocprofv3 --pmc output directories
 """
@@ -556,6 +558,55 @@ def sdpa_backend(q, k, v, torch, F):
     return None
 
 
+def run_sdpa_dense(args):
+    """Context for the MFMA fractions: torch's fused SDPA (flash backend, else
+    memory-efficient; never math) on dense causal attention at long S, the
+    same shapes' head dims and dtypes as the BASELINE configs. FLOPs: 4·D per
+    causal (query, key) pair forward, 14·D forward+backward (the counts the
+    sqrt(N) op's figures use); one JSON line per shape."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import sdpa_kernel
+    dev = torch.device("cuda", 0)
+    for (B, H, S, D, dtype) in ((1, 16, 16384, 128, torch.float16),
+                                (1, 16, 32768, 128, torch.float16),
+                                (2, 32, 8192, 128, torch.bfloat16),
+                                (1, 12, 32768, 64, torch.float16)):
+        g = torch.Generator(device=dev).manual_seed(0)
+        q, k, v, do = (torch.randn(B, H, S, D, generator=g, device=dev, dtype=dtype)
+                       for _ in range(4))
+        backend = sdpa_backend(q, k, v, torch, F)
+        if backend is None:
+            print(json.dumps({"B": B, "H": H, "S": S, "D": D, "sdpa_backend": None}), flush=True)
+            continue
+
+        def fwd(a, b_, c):
+            with sdpa_kernel([backend]):
+                return F.scaled_dot_product_attention(a, b_, c, is_causal=True)
+
+        st = torch.cuda.current_stream()
+        with torch.no_grad():
+            t_f = timed(lambda: fwd(q, k, v), args.steps, args.warmup, torch)
+        qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+        def step():
+            qg.grad = kg.grad = vg.grad = None
+            fwd(qg, kg, vg).backward(do)
+
+        t_t = timed(step, args.steps, args.warmup, torch)
+        pairs = S * (S + 1) // 2 * B * H
+        ff, ft = 4 * D * pairs, 14 * D * pairs
+        print(json.dumps({
+            "B": B, "H": H, "S": S, "D": D, "dtype": str(dtype).split(".")[-1],
+            "sdpa_backend": str(backend).split(".")[-1], "causal": True,
+            "fwd_ms": round(t_f, 4), "fwd_tflops": round(ff / (t_f * 1e-3) / 1e12, 1),
+            "fwd_frac": round(ff / (t_f * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            "train_ms": round(t_t, 4), "train_tflops": round(ft / (t_t * 1e-3) / 1e12, 1),
+            "train_frac": round(ft / (t_t * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)}), flush=True)
+        del q, k, v, do, qg, kg, vg
+        torch.cuda.empty_cache()
+
+
 def first_win(points, key_a, key_b):
     """Smallest S from which a is faster than b at every larger swept S."""
     win = None
@@ -624,6 +675,8 @@ def main(argv=None):
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="CPU baseline threads (default: OMP_NUM_THREADS, else all allowed CPUs)")
     ap.add_argument("--crossover", action="store_true")
+    ap.add_argument("--sdpa-dense", action="store_true",
+                    help="time torch's fused SDPA on dense causal attention at long S (context)")
     ap.add_argument("--config", default=None, metavar="N[,N]|all",
                     help="time the BASELINE configurations 2-5 at every listed S instead")
     ap.add_argument("--profile-workload", action="store_true",
@@ -642,6 +695,8 @@ def main(argv=None):
         run_configs(args)
     elif args.crossover:
         run_crossover(args)
+    elif args.sdpa_dense:
+        run_sdpa_dense(args)
     elif args.profile_workload:
         run_profile_workload(args)
     else:
