@@ -2,6 +2,7 @@
 include/cra.h declares, and rejects bad arguments with the documented codes
 before touching the device."""
 import ctypes
+import math
 import os
 import re
 
@@ -116,6 +117,35 @@ def test_head_span_limit():
     rc = lib.cra_bwd(p, good, good, good, good, wide, 0x10000, 0x10000, 0x10000, 0x10000, None,
                      good, good, good, None, 0x10000, need, None)
     assert rc == N.E_LAYOUT and "dout" in lib.cra_last_error().decode()
+
+
+def _chunks(lib, **kw):
+    """Query chunks of the global-row kernel that cra_bwd_workspace_bytes
+    planned: the workspace is -Delta and -lse*log2(e) (fp32 per query, each
+    256-byte aligned) followed by nchunk fp32 partials of 2*D per global row."""
+    p = prob(**kw)
+    need = lib.cra_bwd_workspace_bytes(ctypes.byref(p))
+    per_query = (p.B * p.H_q * p.S * 4 + 255) // 256 * 256
+    per_chunk = p.B * p.H_kv * lib.cra_global_rows(ctypes.byref(p)) * 2 * p.D * 4
+    assert (need - 2 * per_query) % per_chunk == 0
+    return (need - 2 * per_query) // per_chunk
+
+
+def test_global_row_chunk_rule():
+    """About 1.5 rounds of the global-row kernel's resident workgroups (256
+    CUs; one 192-row workgroup per CU at D = 128, two 128-row ones below), at
+    least one chunk per 6144 queries, at most one per 256 (the shapes of the
+    measured sweep)."""
+    lib = N.load_library()
+    w = lambda S: int(math.ceil(math.sqrt(S)))
+    assert _chunks(lib, B=1, H_q=16, H_kv=16, S=131072, D=128, W=w(131072)) == 22
+    assert _chunks(lib, B=1, H_q=12, H_kv=12, S=8192, D=64, W=w(8192)) == 22
+    assert _chunks(lib, B=1, H_q=12, H_kv=12, S=32768, D=64, W=w(32768)) == 13
+    assert _chunks(lib, B=2, H_q=32, H_kv=32, S=4096, D=128, W=w(4096)) == 6
+    assert _chunks(lib, B=2, H_q=32, H_kv=32, S=65536, D=128, W=w(65536)) == 11
+    assert _chunks(lib, B=1, H_q=8, H_kv=8, S=16384, D=64, W=w(16384)) == 32
+    # short sequences: at most one chunk per 256 queries
+    assert _chunks(lib, B=1, H_q=1, H_kv=1, S=200, D=64, W=w(200), relay=0) == 1
 
 
 def test_bwd_rejects_small_workspace():
