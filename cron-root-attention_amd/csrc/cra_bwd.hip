@@ -995,31 +995,36 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
         }
       }
     }
+    Frag<T> pf[KB], sf[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       const float pv[8] = {p[0][kb][0], p[0][kb][1], p[0][kb][2], p[0][kb][3],
                            p[1][kb][0], p[1][kb][1], p[1][kb][2], p[1][kb][3]};
       const float sv[8] = {ds[0][kb][0], ds[0][kb][1], ds[0][kb][2], ds[0][kb][3],
                            ds[1][kb][0], ds[1][kb][1], ds[1][kb][2], ds[1][kb][3]};
-      const Frag<T> pf = pack8<T>(pv);
-      const Frag<T> sf = pack8<T>(sv);
-      Frag<T> ot[PF + 1], qt[PF + 1];
-      auto tr_pair = [&](int db, Frag<T>& o_, Frag<T>& q_) {
-        const char* po = tO + (2 * qs) * Tile::kBlk16 + lo.tr[db];
-        const char* pq = tQ + (2 * qs) * Tile::kBlk16 + lo.tr[db];
-        o_ = Tile::template tr_frag_at<T>(po, po + Tile::kBlk16);
-        q_ = Tile::template tr_frag_at<T>(pq, pq + Tile::kBlk16);
-      };
+      pf[kb] = pack8<T>(pv);
+      sf[kb] = pack8<T>(sv);
+    }
+    // each transposed Q/dO fragment pair serves every key block of the wave
+    Frag<T> ot[PF + 1], qt[PF + 1];
+    auto tr_pair = [&](int db, Frag<T>& o_, Frag<T>& q_) {
+      const char* po = tO + (2 * qs) * Tile::kBlk16 + lo.tr[db];
+      const char* pq = tQ + (2 * qs) * Tile::kBlk16 + lo.tr[db];
+      o_ = Tile::template tr_frag_at<T>(po, po + Tile::kBlk16);
+      q_ = Tile::template tr_frag_at<T>(pq, pq + Tile::kBlk16);
+    };
 #pragma unroll
-      for (int db = 0; db < PF; ++db) tr_pair(db, ot[db], qt[db]);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int db = 0; db < PF; ++db) tr_pair(db, ot[db], qt[db]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int db = 0; db < D / 16; ++db) {
-        if (db + PF < D / 16) tr_pair(db + PF, ot[(db + PF) % (PF + 1)], qt[(db + PF) % (PF + 1)]);
-        dva[db][kb] = mma(dva[db][kb], ot[db % (PF + 1)], pf);
-        dka[db][kb] = mma(dka[db][kb], qt[db % (PF + 1)], sf);
-        __builtin_amdgcn_sched_barrier(0);
+    for (int db = 0; db < D / 16; ++db) {
+      if (db + PF < D / 16) tr_pair(db + PF, ot[(db + PF) % (PF + 1)], qt[(db + PF) % (PF + 1)]);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        dva[db][kb] = mma(dva[db][kb], ot[db % (PF + 1)], pf[kb]);
+        dka[db][kb] = mma(dka[db][kb], qt[db % (PF + 1)], sf[kb]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -1299,10 +1304,17 @@ void dkdv2_kernel(BwdArgs a) {
 // D = 64), so two 8-wave workgroups share a CU at 4 waves per SIMD, where
 // one 12-wave workgroup left it at 3: backward 1.4% faster at B=1 H=12
 // S=131072 D=64 and 3.3% at H=8 S=65536 (16-wave workgroups: 0.8%).
+// Below D = 128 the local kernel's waves take 32 key rows each (two 16-key
+// blocks sharing every Q/dO fragment read from LDS; 168 VGPRs, 3 waves per
+// SIMD): twice the MFMAs per LDS read and per barrier of its 32-query
+// tiles. Config 4 training (B=1 H=12 D=64) 1.2-1.7% faster at S = 8192,
+// 32768 and 131072 (three alternating runs).
 template <int D>
 constexpr int kDkdvGlobWaves = D == 128 ? 12 : 8;
 constexpr int kDkdvLocalWaves = 4;
-constexpr int kDkdvKB = 1;  // 16-key blocks per wave
+constexpr int kDkdvKB = 1;  // 16-key blocks per wave (global-row kernel)
+template <int D>
+constexpr int kDkdvLocalKB = D == 128 ? 1 : 2;  // local kernel
 constexpr int kDqWaves = 4;
 constexpr int kDqQB = 2;    // 16-query blocks per dQ wave
 constexpr int kDqBN = 64;   // key rows per dQ tile
@@ -1331,7 +1343,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   set_items(aq.docs, [&](int d) { return (a.docs.len[d] + kQM - 1) / kQM; });
   constexpr bool kMfma = sizeof(T) == 2;
   constexpr int kGK = kMfma ? 16 * kDkdvGlobWaves<D> * kDkdvKB : Tr::kBK;   // rows per workgroup
-  constexpr int kLK = kMfma ? 16 * kDkdvLocalWaves * kDkdvKB : Tr::kBK;
+  constexpr int kLK = kMfma ? 16 * kDkdvLocalWaves * kDkdvLocalKB<D> : Tr::kBK;
   set_items(ag.docs, [&](int d) {
     const int g = (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d] * a.docs.rpb[d];
     return (g + kGK - 1) / kGK * a.nchunk;
@@ -1359,7 +1371,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   }
   if (a.dalpha) hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvLocalWaves, kDkdvKB, kDkdvLocalBQ>),
+    hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvLocalWaves, kDkdvLocalKB<D>, kDkdvLocalBQ>),
                        dim3(nl * a.B * a.Hkv), dim3(64 * kDkdvLocalWaves), 0, st, al);
   else
     hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(nl * a.B * a.Hkv), dim3(256), 0, st, al);
@@ -1431,9 +1443,10 @@ bool bwd_tile_config(int dtype, int D, int out[9]) {
     for (int i = 0; i < 9; ++i) out[i] = v[i];
   } else {
     const int gw = D == 128 ? kDkdvGlobWaves<128> : kDkdvGlobWaves<64>;
-    const int v[9] = {kDqWaves,        16 * kDqWaves * kDqQB,           kDqBN,
-                      gw,              16 * gw * kDkdvKB,               kDkdvGlobBQ,
-                      kDkdvLocalWaves, 16 * kDkdvLocalWaves * kDkdvKB, kDkdvLocalBQ};
+    const int lkb = D == 128 ? kDkdvLocalKB<128> : kDkdvLocalKB<64>;
+    const int v[9] = {kDqWaves,        16 * kDqWaves * kDqQB,        kDqBN,
+                      gw,              16 * gw * kDkdvKB,            kDkdvGlobBQ,
+                      kDkdvLocalWaves, 16 * kDkdvLocalWaves * lkb,   kDkdvLocalBQ};
     for (int i = 0; i < 9; ++i) out[i] = v[i];
   }
   return true;

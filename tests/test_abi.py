@@ -281,6 +281,8 @@ def test_tile_config_reports_compiled_geometry():
     h64 = N.tile_config(torch.float16, 64)   # 4 waves per SIMD below D = 128
     assert (h64["dkdv_global_waves"], h64["dkdv_global_rows"]) == (8, 128)
     assert (h["dkdv_local_waves"], h["dkdv_local_keys"], h["dkdv_local_query_tile"]) == (4, 64, 32)
+    # below D = 128 each local wave takes two 16-key blocks
+    assert (h64["dkdv_local_waves"], h64["dkdv_local_keys"]) == (4, 128)
     lib = N.load_library()
     out = N.CraTileConfig()
     assert lib.cra_tile_config(0, 48, ctypes.byref(out)) == N.E_UNSUPPORTED
