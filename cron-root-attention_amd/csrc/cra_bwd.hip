@@ -648,7 +648,7 @@ __device__ __forceinline__ void dq2_tile(const char* tK, const char* tV, const L
                                          const Frag<T> (&df)[QB][D / 32],
                                          f32x4 (&dqa)[D / 16][QB], const float (&lse2)[QB],
                                          const float (&ndl)[QB], float c2, int g,
-                                         const TileMask& mk, bool half0, bool half1) {
+                                         const TileMask<QB>& mk, bool half0, bool half1) {
   using Tile = SwzTile<D, BN>;
   constexpr int NC = D / 32;
 #pragma unroll
@@ -872,7 +872,7 @@ void dq2_kernel(BwdArgs a) {
     const int ts = loc ? lo_k + (nloc - 1 - (it - nglob)) * kBN : it * kBN;
     const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
     const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
-    TileMask mk;
+    TileMask<QB> mk;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       mk.hi[qb] = loc ? qi[qb] - ts : glen[qb] - 1 - ts;

@@ -344,9 +344,10 @@ struct SwzTile {
 // lane's query iff (unsigned)(hi - ko) <= span. Local window: hi = qi - ts,
 // span = W - 1 (qi - W + 1 <= ts + ko <= qi); global prefix: hi = glen - 1 - ts,
 // span = 2^31 - 1 (ts + ko < glen).
+template <int NQB = 2>  // query blocks of the wave
 struct TileMask {
-  int hi[2];
-  unsigned span[2];
+  int hi[NQB];
+  unsigned span[NQB];
   __device__ __forceinline__ bool ok(int ko, int qb) const {
     return (unsigned)(hi[qb] - ko) <= span[qb];
   }

@@ -351,7 +351,7 @@ __device__ __forceinline__ float half_sum(const Frag<T>& pk, const Frag<T>& one)
 // values over the half's 32 keys (the P.V operand and its normaliser).
 template <typename T, bool MASK>
 __device__ __forceinline__ void half_exp(f32x4 (&s)[2][2], int kc, int qb, float c2, float m,
-                                         int g, const TileMask& mk, const Frag<T>& one,
+                                         int g, const TileMask<2>& mk, const Frag<T>& one,
                                          Frag<T>& pk, float& ps) {
   float pv[8];
 #pragma unroll
@@ -412,7 +412,7 @@ __device__ __forceinline__ void attend_tile2(const char* tK, const char* tV, con
                                              const Frag<T> (&qf)[2][D / 32],
                                              f32x4 (&acc)[D / 16][2], float (&m_run)[2],
                                              float (&l_run)[2], float c2, int g,
-                                             const TileMask& mk, const Frag<T>& one) {
+                                             const TileMask<2>& mk, const Frag<T>& one) {
   using Tile = SwzTile<D, BN>;
   constexpr int kHalves = BN / 32;
   f32x4 s[kHalves][2][2];
@@ -445,7 +445,7 @@ __device__ __forceinline__ void attend_half(const char* tK, const char* tV, int 
                                             const Fwd2Lane<D>& lo, const Frag<T> (&qf)[2][D / 32],
                                             f32x4 (&acc)[D / 16][2], float (&m_run)[2],
                                             float (&l_run)[2], float c2, int g,
-                                            const TileMask& mk, const Frag<T>& one) {
+                                            const TileMask<2>& mk, const Frag<T>& one) {
   using Tile = SwzTile<D, BN>;
   f32x4 s[2][2];
   tile_scores<T, D, BN>(tK, lo, qf, kc, s);
@@ -590,7 +590,7 @@ __device__ __forceinline__ void fwd2_item(const FwdArgs& a, const int item, FwdS
     const int ts = loc ? lo_k + (nloc - 1 - (it - nglob)) * kBN : it * kBN;
     const bool work = active && (loc ? (ts <= q_last && ts + kBN - 1 >= w_lo) : ts < wg_hi);
     const bool full = loc ? (ts >= q_last - W + 1 && ts + kBN - 1 <= q0) : ts + kBN <= wg_lo;
-    TileMask mk;
+    TileMask<2> mk;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       mk.hi[qb] = loc ? qi[qb] - ts : glen[qb] - 1 - ts;
