@@ -10,7 +10,8 @@
 //
 // This build keeps every accumulation in fp32 and rounds once:
 //   1. delta_kernel      Delta = rowsum(O * dO)  (fp32 inputs; for fp16/bf16
-//                        dq2_kernel computes Delta of its queries and stores it)
+//                        dq2_kernel computes Delta of its queries and stores
+//                        -Delta and -lse * log2(e) for the dK/dV kernels)
 //   2. dq_kernel         query-centric: local band + global prefix -> dQ
 //   3. dkdv_kernel<GLOB> packed global rows (strided + relay), query range
 //                        split in chunks -> fp32 partials in the workspace
@@ -1331,7 +1332,8 @@ template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   using Tr = BwdTraits<T, D>;
   constexpr int kRows = 256 / (D / 8);
-  // fp16/bf16: dq2_kernel computes Delta for its own queries and stores it
+  // fp16/bf16: dq2_kernel computes Delta for its own queries and stores -Delta
+  // (with -lse * log2(e)) for the dK/dV kernels
   if (sizeof(T) == 4 && a.group == 0)
     hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq),
                        dim3(256), 0, st, a);
@@ -1428,7 +1430,8 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
 }
 
 size_t bwd_workspace_layout(int D, int B, int Hq, int Hkv, int S, int64_t G, int nchunk) {
-  // Delta and -lse * log2(e) per query, then the chunk partials
+  // Delta (2-byte path: -Delta) and -lse * log2(e) per query, then the chunk
+  // partials
   const size_t delta = (((size_t)B * Hq * S * 4) + 255) / 256 * 256;
   const size_t part = (size_t)nchunk * B * Hkv * G * 2 * D * 4;
   return 2 * delta + part;

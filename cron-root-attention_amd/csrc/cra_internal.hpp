@@ -131,8 +131,9 @@ hipError_t launch_bwd(int dtype, int D, const BwdArgs& a, hipStream_t st);
 // receives the query chunks per document of the global-row kernel.
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
                            const int* W, const int* rpb, int64_t G, int* nchunk);
-// Workspace of the backward with nchunk query chunks: Delta [B*Hq*S] fp32
-// (rounded up to 256 bytes), then the partials [nchunk, B, Hkv, G, 2, D] fp32.
+// Workspace of the backward with nchunk query chunks: Delta and -lse*log2(e),
+// [B*Hq*S] fp32 each (rounded up to 256 bytes), then the partials
+// [nchunk, B, Hkv, G, 2, D] fp32.
 size_t bwd_workspace_layout(int D, int B, int Hq, int Hkv, int S, int64_t G, int nchunk);
 
 }  // namespace cra
