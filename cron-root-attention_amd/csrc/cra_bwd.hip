@@ -958,7 +958,7 @@ __device__ __forceinline__ void dkdv2_tile(const char* tQ, const char* tO, const
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // Each subtile's scores, then its exponentials, in sequence: 160 VGPRs,
+  // Each subtile's scores, then its exponentials, in sequence: 165 VGPRs,
   // 3 waves per SIMD. (A software pipeline over the subtiles, the next
   // subtile's score MFMAs beside this one's exponentials, needs 225
   // registers and 2 waves per SIMD: 4.2% slower backward with the local
@@ -1291,7 +1291,7 @@ void dkdv2_kernel(BwdArgs a) {
 
 // dK/dV workgroups: waves of 16 key rows (no register file spill into AGPR
 // copies at D = 128; 32 rows per wave measured 14% slower). The global-row
-// kernel uses 12 waves (192 rows): at 160 VGPRs a SIMD holds 3 of its
+// kernel uses 12 waves (192 rows): at 164 VGPRs a SIMD holds 3 of its
 // waves, and one 12-wave workgroup fills them, where a second 8-wave
 // workgroup did not fit beside the first (8 waves measured 1.7% slower
 // backward, 4 waves 3% slower than 8); the local
@@ -1301,7 +1301,7 @@ void dkdv2_kernel(BwdArgs a) {
 // fragment read from LDS serves two query blocks). 16 queries per wave
 // lose that reuse: 8 waves measured 27% slower, and with 32-key tiles at
 // 3 or 4 waves per SIMD still 5-10% slower backward at D = 128.
-// Below D = 128 the global-row kernel needs at most 128 VGPRs (112 at
+// Below D = 128 the global-row kernel needs at most 128 VGPRs (114 at
 // D = 64), so two 8-wave workgroups share a CU at 4 waves per SIMD, where
 // one 12-wave workgroup left it at 3: backward 1.4% faster at B=1 H=12
 // S=131072 D=64 and 3.3% at H=8 S=65536 (16-wave workgroups: 0.8%).
@@ -1321,7 +1321,7 @@ constexpr int kDqQB = 2;    // 16-query blocks per dQ wave
 constexpr int kDqBN = 64;   // key rows per dQ tile
 constexpr int kDqWPE = 2;   // dQ waves per SIMD (register budget)
 // Query rows per dK/dV tile. The local kernel's 32-row tiles keep its LDS
-// at 33 KB, so three 4-wave workgroups (3 waves per SIMD, 160 VGPRs) fit on
+// at 33 KB, so three 4-wave workgroups (3 waves per SIMD, 165 VGPRs) fit on
 // a CU; with 64-row tiles only two fit. The global-row kernel (one 12-wave
 // workgroup per CU, 130 KB of LDS) takes 128-row tiles: one barrier per 128
 // queries instead of 64 (backward 1.7% faster).
