@@ -333,6 +333,29 @@ def test_ns_backward_rows_match_oracle():
     check_grad_rows(q, k, v, do, dq, dk, dv, plan, 0, [0, 15], doubled=doubled)
 
 
+@pytest.mark.parametrize("B,H,S,D,chunks", [(1, 1, 65536, 128, 96), (4, 32, 4096, 64, 3)])
+def test_backward_rows_at_chunk_count_extremes(B, H, S, D, chunks):
+    """The global-row kernel's query-chunk count follows the problem: one
+    head of S = 65536 is cut into 96 chunks (each row's gradient then sums up
+    to 96 partials), 128 heads of S = 4096 into 3. Gradient spot rows of the
+    first and last head against the fp64 oracle in both cases."""
+    import ctypes
+    say(f"backward rows, {chunks} query chunks: B={B} H={H} S={S} D={D}")
+    p = _native.problem(B, H, H, S, D, O.window_size(S), S > 2048, 2, torch.float16,
+                        1 / math.sqrt(D))
+    lib = _native.load_library()
+    per_query = (B * H * S * 4 + 255) // 256 * 256
+    per_chunk = B * H * int(_native.global_rows(p)) * 2 * D * 4
+    assert (lib.cra_bwd_workspace_bytes(ctypes.byref(p)) - 2 * per_query) // per_chunk == chunks
+    q, k, v, do = device_inputs(B, H, H, S, D, F16, seed=3, with_do=True)
+    plan = plan_for(S)
+    qd, kd, vd = (t.clone().requires_grad_(True) for t in (q, k, v))
+    cra.cron_root_attention(qd, kd, vd).backward(do)
+    for t in (qd.grad, kd.grad, vd.grad):
+        assert torch.isfinite(t).all()
+    check_grad_rows(q, k, v, do, qd.grad, kd.grad, vd.grad, plan, B - 1, sorted({0, H - 1}))
+
+
 @pytest.mark.parametrize("B,H,S,dtype,bwd", [(1, 16, 524288, F16, True), (2, 32, 262144, BF16, False)])
 def test_largest_baseline_shapes(B, H, S, dtype, bwd):
     """BASELINE's largest configurations (config 3 at S=524288 with the
