@@ -30,6 +30,43 @@ int hip_fail(hipError_t e, const char* where) {
   return fail(CRA_E_HIP, "%s: %s", where, hipGetErrorString(e));
 }
 
+// Compute units of the current device, looked up once per device. The
+// backward's query-chunk rule sizes its work to the resident workgroup slots
+// of the device it runs on. With no device to ask (a host without a GPU
+// planning a workspace) the MI355X's 256 stands in: planning only, nothing
+// is launched then.
+constexpr int kMaxCuDevices = 64;
+std::mutex g_cu_mu;
+int g_cu_count[kMaxCuDevices] = {};
+
+int device_cus() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxCuDevices) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(g_cu_mu);
+  if (!g_cu_count[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1) {
+      (void)hipGetLastError();
+      return 256;
+    }
+    g_cu_count[dev] = cus;
+  }
+  return g_cu_count[dev];
+}
+
+}  // namespace
+
+namespace cra {
+// Error text for the host-only translation units (the CPU-tensor path).
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace cra
+
+namespace {
+
 int elem_size(int dtype) { return dtype == CRA_F32 ? 4 : 2; }
 
 // Fields every entry point needs; W and relay are checked by the plain
@@ -196,7 +233,7 @@ cra::Docs group_table(const Plan& pl, int g) {
 
 size_t workspace_bytes(const cra_problem* p, const Plan& pl, int* nchunk) {
   return cra::bwd_workspace_bytes(p->D, p->B, p->H_q, p->H_kv, p->S, pl.n, pl.len.data(),
-                                  pl.W.data(), pl.rpb.data(), pl.G, nchunk);
+                                  pl.W.data(), pl.rpb.data(), pl.G, device_cus(), nchunk);
 }
 
 int build_global_impl(const cra_problem* p, const Plan& pl, cra_tensor k, cra_tensor v,

@@ -1393,7 +1393,7 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
 }  // namespace
 
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
-                           const int* W, const int* rpb, int64_t G, int* nchunk) {
+                           const int* W, const int* rpb, int64_t G, int cus, int* nchunk) {
   // Query chunks of the global-row kernel: each document's query range is
   // cut into the same number of chunks (multiples of 64 queries), one
   // workgroup per (row tile, chunk). More chunks balance the uneven
@@ -1401,16 +1401,16 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
   // shorten the last round; each chunk costs a partial dK/dV of its rows,
   // written once and summed once by gsum_kernel. Measured on gfx950 over
   // 1-48 chunks (training step, 2 sweeps): the best counts fill the kernel's
-  // resident slots about 1.5 times over (256 CUs, one 12-wave workgroup per
-  // CU at D = 128, two 8-wave ones below) until chunks would exceed about
-  // 6144 queries, from which on 6144-query chunks keep the balance:
+  // resident slots about 1.5 times over (the device's CUs, one 12-wave
+  // workgroup per CU at D = 128, two 8-wave ones below) until chunks would
+  // exceed about 6144 queries, from which on 6144-query chunks keep the
+  // balance. On the 256-CU MI355X:
   //   B=1 H=16 D=128 S=131072: 22 chunks (16 and 32 within 0.6%)
   //   B=1 H=12 D=64 S=8192 / 32768 / 131072: 22 / 13 / 22 chunks
   //   B=2 H=32 D=128 S=4096: 6 (the previous rule's 16 was 12% slower)
   //   B=1 H=8 D=64 S=16384: 32 (64 was 10% slower)
-  constexpr int kCUs = 256;
   const int rows = D == 128 ? 16 * kDkdvGlobWaves<128> * kDkdvKB : 16 * kDkdvGlobWaves<64> * kDkdvKB;
-  const int slots = kCUs * (D == 128 ? 1 : 2);
+  const int slots = (cus > 0 ? cus : 256) * (D == 128 ? 1 : 2);
   int64_t row_tiles = 0;
   int max_len = 1;
   for (int d = 0; d < n; ++d) {

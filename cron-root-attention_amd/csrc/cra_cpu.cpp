@@ -19,10 +19,16 @@
 
 #include <algorithm>
 #include <atomic>
+#include <new>
 #include <thread>
 #include <vector>
 
 #include "../../include/cra.h"
+
+namespace cra {
+// Sets the calling thread's cra_last_error() text (defined beside the C ABI).
+int set_error(int code, const char* msg);
+}  // namespace cra
 
 namespace {
 
@@ -247,31 +253,55 @@ void attend_rows(const cra_problem* p, cra_tensor q, cra_tensor o, int b, int h,
 
 }  // namespace
 
-extern "C" int cra_fwd_cpu(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
-                           cra_tensor o, int32_t threads) {
-  if (!p || !q.ptr || !k.ptr || !v.ptr || !o.ptr) return CRA_E_INVALID;
-  if (p->dtype != CRA_F16 && p->dtype != CRA_BF16 && p->dtype != CRA_F32) return CRA_E_DTYPE;
-  if (p->B < 1 || p->H_q < 1 || p->H_kv < 1 || p->S < 1 || p->D < 1 || p->H_q % p->H_kv ||
-      p->W < 1 || p->W > p->S || (p->relay && (p->top_k < 1 || p->top_k > 4)) ||
-      !(p->scale > 0.f))
-    return CRA_E_INVALID;
+namespace {
+
+int fwd_cpu_impl(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_tensor o,
+                 int32_t threads) {
+  if (!p) return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: problem is NULL");
+  if (!q.ptr || !k.ptr || !v.ptr || !o.ptr)
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: q, k, v and o must not be NULL");
+  if (p->dtype != CRA_F16 && p->dtype != CRA_BF16 && p->dtype != CRA_F32)
+    return cra::set_error(CRA_E_DTYPE, "cra_fwd_cpu: unknown dtype code");
+  if (p->B < 1 || p->H_q < 1 || p->H_kv < 1 || p->S < 1 || p->D < 1)
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: B, H_q, H_kv, S and D must be >= 1");
+  if (p->H_q % p->H_kv)
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: H_q must be a multiple of H_kv");
+  if (p->W < 1 || p->W > p->S)
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: window W outside [1, S]");
+  if (p->relay && (p->top_k < 1 || p->top_k > 4))
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: top_k outside [1, 4]");
+  if (!(p->scale > 0.f)) return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: scale must be > 0");
   const int groups = p->H_q / p->H_kv;
   const int nthr = std::max(1, threads);
   // kv heads first (each shared by its query heads), then query blocks
   std::vector<KvHead> heads((size_t)p->B * p->H_kv);
   std::atomic<int> next{0};
+  std::atomic<bool> failed{false};
   auto run = [&](auto&& body, int n) {
     next = 0;
     std::vector<std::thread> pool;
     const int nt = std::min(nthr, n);
-    for (int t = 0; t < nt; ++t)
-      pool.emplace_back([&] {
+    // an exception may not leave a thread's function: the item fails the call
+    auto work = [&] {
+      try {
         for (int i = next++; i < n; i = next++) body(i);
-      });
+      } catch (...) {
+        failed = true;
+        next = n;
+      }
+    };
+    try {
+      for (int t = 1; t < nt; ++t) pool.emplace_back(work);
+    } catch (...) {
+      // fewer workers than asked (thread creation failed): the ones started
+      // and this thread still take every item
+    }
+    work();
     for (auto& th : pool) th.join();
   };
   run([&](int i) { build_kv_head(p, k, v, i / p->H_kv, i % p->H_kv, &heads[i]); },
       p->B * p->H_kv);
+  if (failed) return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: out of host memory");
   constexpr int kChunk = 256;
   const int nch = (p->S + kChunk - 1) / kChunk;
   run(
@@ -283,5 +313,20 @@ extern "C" int cra_fwd_cpu(const cra_problem* p, cra_tensor q, cra_tensor k, cra
                     std::min(p->S, (c + 1) * kChunk), qrow, sc, acc);
       },
       p->B * p->H_q * nch);
+  if (failed) return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: out of host memory");
   return CRA_OK;
+}
+
+}  // namespace
+
+// No exception crosses the C ABI: an allocation failure becomes an error code.
+extern "C" int cra_fwd_cpu(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v,
+                           cra_tensor o, int32_t threads) {
+  try {
+    return fwd_cpu_impl(p, q, k, v, o, threads);
+  } catch (const std::bad_alloc&) {
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: out of host memory");
+  } catch (...) {
+    return cra::set_error(CRA_E_INVALID, "cra_fwd_cpu: host error");
+  }
 }

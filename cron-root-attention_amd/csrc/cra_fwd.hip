@@ -21,6 +21,7 @@
 // per query grows with i) and consecutive workgroups are different heads of
 // the same tile, so each XCD keeps a fixed pair of heads.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "cra_common.hpp"
@@ -667,6 +668,31 @@ void fwd2_persistent_kernel(FwdArgs a) {
   }
 }
 
+// Resident workgroups of `kern` on the current device (CUs x workgroups per
+// CU), looked up once per device and instantiation: the persistent launch
+// serves small problems, where per-call host queries would cost more than
+// the kernel.
+template <typename T, int D, typename K>
+hipError_t resident_slots(K kern, int threads, int* out) {
+  constexpr int kMaxDev = 64;
+  static std::mutex mu;
+  static int cache[kMaxDev] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    int per_cu = 0, cus = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    cache[dev] = std::max(1, per_cu) * std::max(1, cus);
+  }
+  *out = cache[dev];
+  return hipSuccess;
+}
+
 // Waves per forward workgroup (32 queries each) for 2-byte types. 8 waves
 // (256 queries sharing each K/V tile) halve the tile loads per query but
 // measured 4% slower at D = 128: the wider local window adds key tiles.
@@ -685,14 +711,11 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
       if (a.work_counter && a.phases == 3) {
         // one round of resident workgroups: CUs x workgroups per CU
         auto kern = fwd2_persistent_kernel<T, Dc, kFwdWaves>;
-        int per_cu = 0, dev = 0, cus = 0;
-        qerr = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * kFwdWaves, 0);
-        if (qerr == hipSuccess) qerr = hipGetDevice(&dev);
-        if (qerr == hipSuccess)
-          qerr = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        int slots = 0;
+        qerr = resident_slots<T, Dc>(kern, 64 * kFwdWaves, &slots);
         if (qerr != hipSuccess) return;
         const int items = (int)grid.x;
-        const dim3 pgrid(std::max(1, std::min(items, std::max(1, per_cu) * cus)));
+        const dim3 pgrid(std::max(1, std::min(items, slots)));
         hipLaunchKernelGGL(kern, pgrid, block, 0, st, b);
         return;
       }

@@ -127,10 +127,11 @@ hipError_t launch_build_global(int dtype, int D, const GlobalArgs& a, int B, hip
 hipError_t launch_fwd(int dtype, int D, const FwdArgs& a, hipStream_t st);
 hipError_t launch_bwd(int dtype, int D, const BwdArgs& a, hipStream_t st);
 // Workspace of the backward for n documents of lengths len[], windows W[]
-// and packed rows per block rpb[] (G packed rows per head in total); *nchunk
-// receives the query chunks per document of the global-row kernel.
+// and packed rows per block rpb[] (G packed rows per head in total) on a
+// device with `cus` compute units; *nchunk receives the query chunks per
+// document of the global-row kernel.
 size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const int* len,
-                           const int* W, const int* rpb, int64_t G, int* nchunk);
+                           const int* W, const int* rpb, int64_t G, int cus, int* nchunk);
 // Workspace of the backward with nchunk query chunks: Delta and -lse*log2(e),
 // [B*Hq*S] fp32 each (rounded up to 256 bytes), then the partials
 // [nchunk, B, Hkv, G, 2, D] fp32.

@@ -152,9 +152,11 @@ int cra_bwd(const cra_problem* p, cra_tensor q, cra_tensor k, cra_tensor v, cra_
 #define CRA_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* cra_bwd without a workspace argument and without any allocation: for
- * callers that cannot allocate device memory (code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc). No counterpart in
- * the reference.
+ * callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. Its use under HIP
+ * graph capture is untested: the first call on a device looks up the
+ * scratch address with hipGetSymbolAddress, so make one call on each device
+ * before any capture.
  * The workspace is a file-scope device array of CRA_NOALLOC_SCRATCH_BYTES
  * (64 MiB) that every device the library runs on holds until the process
  * ends; its address is looked up once per device on the first call there.

@@ -4,8 +4,9 @@ forward check and the gradient spot checks against the fp64 oracle.
 Tolerances (the north star's fp16 figures; bf16/fp32 scaled to their
 precision):
   forward  fp16: max |o - o_ref| <= 2e-3, asserted as written.
-           bf16/fp32: |o - o_ref| <= max(TOL, bound) per element, TOL = 3e-2 /
-           2e-5, and mean |o - o_ref| <= mean(bound) / 2.
+           bf16/fp32: |o - o_ref| <= max(TOL, bound) per element, TOL = 1.6e-2 /
+           2e-5 (bf16: 4 unit roundoffs of 2^-8, the fp16 contract's 2e-3 =
+           4 x 2^-11 scaled to bf16), and mean |o - o_ref| <= mean(bound) / 2.
   lse      fp16 1e-3, bf16 4e-3, fp32 1e-5 (max-abs; the normaliser sums the
            rounded P, so ln l moves by up to one unit roundoff).
   backward ||g - g_ref|| / ||g_ref||  fp16 1e-2, bf16 3e-2, fp32 1e-4, per
@@ -25,7 +26,7 @@ import torch
 from oracle import cra_oracle as O
 
 F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
-TOL_FWD = {F16: 2e-3, BF16: 3e-2, F32: 2e-5}
+TOL_FWD = {F16: 2e-3, BF16: 1.6e-2, F32: 2e-5}
 TOL_GRAD = {F16: 1e-2, BF16: 3e-2, F32: 1e-4}
 # LSE (internal, saved for the backward): the kernels' normaliser sums the
 # rounded P that the P.V products use, so ln(l) may differ from the exact

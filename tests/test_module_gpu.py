@@ -78,6 +78,7 @@ def test_config5_module_hybrid(S, training):
     gen = torch.Generator(device=DEV).manual_seed(S)
     x = torch.randn(B, S, E, generator=gen, device=DEV).to(BF16).requires_grad_(training)
     box, hook = _capture(m.o_proj)
+    grads, ghooks = _capture_grads(m) if training else ({}, [])
     with torch.set_grad_enabled(training):
         y = m(x)
     hook.remove()
@@ -95,9 +96,46 @@ def test_config5_module_hybrid(S, training):
     if training:
         gy = torch.randn(y.shape, generator=gen, device=DEV).to(BF16)
         y.backward(gy)
+        for h in ghooks:
+            h.remove()
         assert bool(torch.isfinite(x.grad).all())
         for p in m.parameters():
             assert bool(torch.isfinite(p.grad).all())
+        if backend == "cron_root" and S <= 4096:
+            _check_attention_grads(q, k, v, grads, B, S, H, D, [(0, 0), (1, 31)])
+
+
+def _capture_grads(m):
+    """Gradients reaching the attention op: dL/dq, dL/dk, dL/dv (the outputs
+    of the three projections) and dL/d(attention output) (the input of the
+    output projection)."""
+    grads = {}
+    hooks = []
+    for name, lin in (("dq", m.q_proj), ("dk", m.k_proj), ("dv", m.v_proj)):
+        def fwd(mod, inp, out, name=name):
+            if out.requires_grad:  # not the test's own recomputation under no_grad
+                out.register_hook(lambda g, name=name: grads.__setitem__(name, g.detach()))
+        hooks.append(lin.register_forward_hook(fwd))
+    hooks.append(m.o_proj.register_full_backward_hook(
+        lambda mod, gin, gout: grads.__setitem__("do", gin[0].detach())))
+    return grads, hooks
+
+
+def _check_attention_grads(q, k, v, grads, B, S, H, D, heads):
+    """The sqrt(N) op's backward inside the module against the fp64 oracle:
+    the q/k/v gradients of each (b, h) in ``heads`` from the attention inputs
+    and output gradient the module produced (bf16), relative error within
+    the bf16 gradient tolerance."""
+    plan = plan_for(S)
+    hd = lambda t: t.view(B, S, H, D).transpose(1, 2)
+    dq, dk, dv, do = (hd(grads[n]) for n in ("dq", "dk", "dv", "do"))
+    for b, h in heads:
+        sl = lambda t: t[b:b + 1, h:h + 1].float().cpu().to(BF16)
+        _, _, _, g = O.forward_backward(sl(q), sl(k), sl(v), sl(do), plan)
+        for name, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+            e = rel_fro(t[b:b + 1, h:h + 1], g[name])
+            say(f"  b={b} h={h} {name}: rel {e:.2e}")
+            assert e <= TOL_GRAD[BF16], (b, h, name, e)
 
 
 # ------------------------------------------------------------- dispatcher
@@ -245,8 +283,9 @@ def test_multihead_attention_matches_oracle(batch_first):
 
 @pytest.mark.parametrize("S", [1500, 3000])
 def test_use_persistent_is_bit_identical(S):
-    """use_persistent=True (the reference's persistent forward, core.py:3548-3569)
-    computes the same function: outputs and gradients bit-identical."""
+    """use_persistent=True (the reference's persistent forward, core.py:711-900,
+    dispatched at core.py:3548-3569): output and gradients against the fp64
+    oracle, and bit-identical to the tiled forward's."""
     q, k, v, do = inputs(1, 4, 4, S, 64, F16, seed=S + 9)
     res = []
     for pers in (False, True):
@@ -256,6 +295,14 @@ def test_use_persistent_is_bit_identical(S):
         res.append((o.detach(), qd.grad, kd.grad, vd.grad))
     for a, b in zip(*res):
         assert torch.equal(a, b)
+    plan = plan_for(S)
+    o_p, dq, dk, dv = res[1]
+    check_forward(o_p.cpu(), q, k, v, plan, F16)
+    _, _, _, g = O.forward_backward(q, k, v, do, plan)
+    for name, t in (("dq", dq), ("dk", dk), ("dv", dv)):
+        e = rel_fro(t, g[name])
+        say(f"  persistent {name}: rel {e:.2e}")
+        assert e <= TOL_GRAD[F16], name
 
 
 @pytest.mark.parametrize("Hq,Hkv,kw", [(4, 2, {}), (4, 2, {"kv_groups": 3}), (3, 2, {"kv_groups": 1})])

@@ -19,7 +19,7 @@ from oracle import cra_oracle as O
 from tests.golden.make_golden import SHAPES, make_inputs
 from tests.parity_util import (BF16, DEV, F16, F32, TOL_FWD, TOL_GRAD, TOL_LSE, check_forward,
                                check_grad_rows, device_inputs, inputs, max_abs, plan_for,
-                               rel_fro, say)
+                               rel_fro, say, spot_ranges)
 
 pytestmark = pytest.mark.gpu
 
@@ -246,18 +246,37 @@ def test_backward_relay_log_scale():
                                            (F16, 1, 16, 2048, 128), (BF16, 1, 4, 5000, 128),
                                            (F16, 1, 2, 9000, 32), (F16, 1, 16, 131072, 128)])
 def test_persistent_forward_bit_identical(dtype, B, H, S, D):
-    """cra_fwd_persistent (work queue over a CU-sized grid) = cra_fwd, bit
-    for bit, with and without relay; a second call with a fresh counter too."""
+    """cra_fwd_persistent (work queue over a CU-sized grid; the reference's
+    persistent forward, core.py:711-900, dispatched at core.py:3548-3569)
+    against the fp64 oracle: every row of every head up to S = 9000, and at
+    the north-star shape three 256-row ranges of heads 0 and 15 (lse too);
+    bit for bit equal to cra_fwd, with and without relay, and a second call
+    with a fresh counter too."""
     say(f"persistent forward {dtype} B={B} H={H} S={S} D={D}")
     q, k, v = device_inputs(B, H, H, S, D, dtype, seed=S)
     plan = plan_for(S)
     p = _native.problem(B, H, H, S, D, plan.W, plan.relay, 2, dtype, 1 / math.sqrt(D))
-    gk, gv, _ = _native.build_global(p, k, v, None)
+    gk, gv, src = _native.build_global(p, k, v, None)
     o, lse = _native.forward(p, q, k, v, gk, gv)
     for _ in range(2):
         op, lsep = _native.forward_persistent(p, q, k, v, gk, gv)
         torch.cuda.synchronize()
         assert torch.equal(op, o) and torch.equal(lsep, lse)
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    if plan.relay:
+        assert torch.equal(src.cpu(), O.relay_select(kc, plan, "lanetree").to(torch.int32))
+    if S <= 9000:
+        _, ref_lse = check_forward(op.cpu(), qc, kc, vc, plan, dtype)
+        assert max_abs(lsep, ref_lse) <= TOL_LSE[dtype]
+    else:
+        heads = [0, H - 1]
+        srch = src.cpu()[:, heads].long()
+        qh, kh, vh, oh = qc[:, heads], kc[:, heads], vc[:, heads], op.cpu()[:, heads]
+        for lo, hi in spot_ranges(S):
+            say(f"  rows [{lo},{hi})")
+            _, ref_lse = check_forward(oh[:, :, lo:hi], qh, kh, vh, plan, dtype,
+                                       rows=(lo, hi), src=srch)
+            assert max_abs(lsep.cpu()[:, heads, lo:hi], ref_lse) <= TOL_LSE[dtype]
 
 
 def test_backward_deterministic():

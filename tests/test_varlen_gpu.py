@@ -28,7 +28,7 @@ from oracle import cra_oracle as O
 pytestmark = pytest.mark.gpu
 
 F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
-TOL_FWD = {F16: 2e-3, BF16: 3e-2, F32: 2e-5}
+TOL_FWD = {F16: 2e-3, BF16: 1.6e-2, F32: 2e-5}  # bf16: 4 unit roundoffs, as fp16's 2e-3
 TOL_GRAD = {F16: 1e-2, BF16: 3e-2, F32: 1e-4}
 UNIT_ROUNDOFF = {F16: 2.0 ** -11, BF16: 2.0 ** -8, F32: 2.0 ** -24}
 REL_SPLIT = {F16: 2e-3, BF16: 1.5e-2, F32: 1e-5}
