@@ -32,7 +32,7 @@ def calibrate(H: int = 8, D: int = 64, dtype=None, S: int = 4096, verbose: bool 
     on a GPU, runs one forward+backward at S to load the kernels.
     """
     dtype = dtype or _torch.float16
-    Dp = next((d for d in (32, 64, 128) if D <= d), D)
+    Dp = next((d for d in (32, 64, 128, 256) if D <= d), D)
     t = _native.tile_config(dtype, Dp)
     if _torch.cuda.is_available():
         dev = _torch.device("cuda", _torch.cuda.current_device())
@@ -41,14 +41,16 @@ def calibrate(H: int = 8, D: int = 64, dtype=None, S: int = 4096, verbose: bool 
         v = _torch.randn(1, H, S, D, device=dev, dtype=dtype, requires_grad=True)
         cron_root_attention_v14(q, k, v).sum().backward()
         _torch.cuda.synchronize(dev)
-    stages = 2  # every kernel double-buffers its streamed tiles in LDS
+    # the gfx950-tiled kernels (fp16/bf16 up to D = 128) double-buffer their
+    # streamed tiles in LDS; the generic ones (fp32, D = 256) stage one tile
+    stages = 2 if (dtype != _torch.float32 and Dp <= 128) else 1
     cfg = {"fwd": (t["fwd_waves"], stages), "bwd": (t["dq_waves"], stages)}
     if verbose:
         print(f"  H={H} D={D}: fwd {t['fwd_waves']} waves x {t['fwd_queries']} queries, "
               f"{t['fwd_key_tile']}-key tiles; dQ {t['dq_waves']} waves x {t['dq_queries']} queries; "
               f"global-row dK/dV {t['dkdv_global_waves']} waves x {t['dkdv_global_rows']} rows; "
               f"local dK/dV {t['dkdv_local_waves']} waves x {t['dkdv_local_keys']} keys "
-              f"(static gfx950 tiles, {stages} LDS stages)")
+              f"(static gfx950 tiles, {stages} LDS stage{'s' if stages > 1 else ''})")
     return cfg
 
 

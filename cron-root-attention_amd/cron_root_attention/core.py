@@ -43,7 +43,7 @@ import torch.nn.functional as F
 from . import _native
 
 RELAY_THRESHOLD = 2048          # core.py:2832
-_SUPPORTED_D = (32, 64, 128)
+_SUPPORTED_D = (32, 64, 128, 256)
 
 # CU counts for the persistent-grid helpers (reference GPU_SM_MAP, core.py:58-135,
 # lists NVIDIA parts only).
@@ -87,7 +87,7 @@ def _padded_head_dim(D: int) -> int:
     for d in _SUPPORTED_D:
         if D <= d:
             return d
-    raise NotImplementedError(f"head dim {D} > 128 is not built for gfx950 in this release")
+    raise NotImplementedError(f"head dim {D} > 256 is not built for gfx950 in this release")
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
@@ -286,7 +286,7 @@ def _op_plan(q, k, v, use_persistent, kv_groups, relay_top_k):
     """(window, relay, top_k, scale) when the call can go to the C++ operator
     ``torch.ops.cra.attention`` (the Function's plan and launches, bit for
     bit, without its Python host cost; it copies layouts the kernels cannot
-    take, as the Function does): q, k, v on one GPU, head dim 32/64/128, the
+    take, as the Function does): q, k, v on one GPU, head dim 32/64/128/256, the
     tiled forward. None sends the call to the Python Function, which also
     raises the reference's errors for invalid arguments."""
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:

@@ -81,7 +81,7 @@ int check_problem_common(const cra_problem* p) {
   if (p->H_q % p->H_kv)
     return fail(CRA_E_INVALID, "H_q (%d) must be a multiple of H_kv (%d)", p->H_q, p->H_kv);
   if (!cra_supported_head_dim(p->D))
-    return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128)", p->D);
+    return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128, 256)", p->D);
   if (!(p->scale > 0.f)) return fail(CRA_E_INVALID, "scale must be > 0");
   // 32-bit row indices inside the kernels
   if ((int64_t)p->B * p->H_q * (int64_t)p->S > (int64_t)1 << 31)
@@ -417,7 +417,7 @@ int scratch_address(void* stream, void** out) {
 
 extern "C" {
 
-int cra_supported_head_dim(int32_t D) { return D == 32 || D == 64 || D == 128; }
+int cra_supported_head_dim(int32_t D) { return D == 32 || D == 64 || D == 128 || D == 256; }
 
 int32_t cra_abi_version(void) { return CRA_ABI_VERSION; }
 
@@ -565,7 +565,7 @@ int cra_tile_config(int32_t dtype, int32_t D, cra_tile_config_t* out) {
     return fail(CRA_E_DTYPE, "unknown dtype code %d", dtype);
   int f[3], b[9];
   if (!cra::fwd_tile_config(dtype, D, f) || !cra::bwd_tile_config(dtype, D, b))
-    return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128)", D);
+    return fail(CRA_E_UNSUPPORTED, "head dim %d not built (32, 64, 128, 256)", D);
   out->fwd_waves = f[0];
   out->fwd_queries = f[1];
   out->fwd_key_tile = f[2];

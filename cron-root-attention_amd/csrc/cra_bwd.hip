@@ -32,15 +32,20 @@ namespace cra {
 
 namespace {
 
-template <typename T, int D>
+// Geometry of the generic (non-gfx950-tiled) kernels: the fp32 path, and
+// every dtype at head dim 256. NB = 16-row blocks per wave (queries for dQ,
+// keys for dK/dV): two below D = 256; one at D = 256, where two would hold
+// 256 VGPRs of accumulators and operands per wave.
+template <typename T, int D, int NB = 2>
 struct BwdTraits {
   static constexpr int kThreads = 256;
-  static constexpr int kQW = 32;                        // dq: queries per wave
-  static constexpr int kBM = 128;                       // dq: queries per workgroup
-  static constexpr int kBN = sizeof(T) == 4 ? 32 : 64;  // dq: key rows per tile
-  static constexpr int kKW = 32;                        // dkdv: key rows per wave
-  static constexpr int kBK = 128;                       // dkdv: key rows per workgroup
-  static constexpr int kBQ = sizeof(T) == 4 ? 32 : 64;  // dkdv: queries per tile
+  static constexpr bool kSmallTiles = sizeof(T) == 4 || D > 128;
+  static constexpr int kQW = 16 * NB;                   // dq: queries per wave
+  static constexpr int kBM = 4 * kQW;                   // dq: queries per workgroup
+  static constexpr int kBN = kSmallTiles ? 32 : 64;     // dq: key rows per tile
+  static constexpr int kKW = 16 * NB;                   // dkdv: key rows per wave
+  static constexpr int kBK = 4 * kKW;                   // dkdv: key rows per workgroup
+  static constexpr int kBQ = kSmallTiles ? 32 : 64;     // dkdv: queries per tile
   static constexpr int kDC = D / 32;
   static constexpr int kDB = D / 16;
   static constexpr int kLD = D + 16 / (int)sizeof(T);
@@ -102,46 +107,46 @@ __global__ __launch_bounds__(256) void delta_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // 2. dQ, query-centric (mirror of the forward's tiling)
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool MASK, typename Valid>
+template <typename T, int D, int NB, bool MASK, typename Valid>
 __device__ __forceinline__ void dq_tile(const T* sK, const T* sV, const T* sKt,
-                                        const Frag<T> (&qf)[2][BwdTraits<T, D>::kDC],
-                                        const Frag<T> (&df)[2][BwdTraits<T, D>::kDC],
-                                        f32x4 (&dqa)[BwdTraits<T, D>::kDB][2],
-                                        const float (&lse2)[2], const float (&dl)[2], float c2,
+                                        const Frag<T> (&qf)[NB][BwdTraits<T, D, NB>::kDC],
+                                        const Frag<T> (&df)[NB][BwdTraits<T, D, NB>::kDC],
+                                        f32x4 (&dqa)[BwdTraits<T, D, NB>::kDB][NB],
+                                        const float (&lse2)[NB], const float (&dl)[NB], float c2,
                                         int l16, int g, Valid valid) {
-  using Tr = BwdTraits<T, D>;
+  using Tr = BwdTraits<T, D, NB>;
   constexpr int kKB = Tr::kBN / 16, kKC = Tr::kBN / 32;
-  Frag<T> dsf[kKC][2];
-  float ds[kKB][2][4];
+  Frag<T> dsf[kKC][NB];
+  float ds[kKB][NB][4];
 #pragma unroll
   for (int kb = 0; kb < kKB; ++kb) {
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, p0 = s0, p1 = s0;
+    f32x4 sc[NB], dp[NB];
+#pragma unroll
+    for (int qb = 0; qb < NB; ++qb) sc[qb] = dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < Tr::kDC; ++c) {
       const Frag<T> kf = lds_frag_row<T>(sK + (16 * kb + l16) * Tr::kLD + 32 * c + 8 * g);
       const Frag<T> vf = lds_frag_row<T>(sV + (16 * kb + l16) * Tr::kLD + 32 * c + 8 * g);
-      s0 = mma(s0, kf, qf[0][c]);
-      s1 = mma(s1, kf, qf[1][c]);
-      p0 = mma(p0, vf, df[0][c]);
-      p1 = mma(p1, vf, df[1][c]);
+#pragma unroll
+      for (int qb = 0; qb < NB; ++qb) sc[qb] = mma(sc[qb], kf, qf[qb][c]);
+#pragma unroll
+      for (int qb = 0; qb < NB; ++qb) dp[qb] = mma(dp[qb], vf, df[qb][c]);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int ko = 16 * kb + 4 * g + r;
-      float x0 = s0[r] * c2 - lse2[0];
-      float x1 = s1[r] * c2 - lse2[1];
-      if (MASK) {
-        if (!valid(ko, 0)) x0 = -__builtin_huge_valf();
-        if (!valid(ko, 1)) x1 = -__builtin_huge_valf();
+#pragma unroll
+      for (int qb = 0; qb < NB; ++qb) {
+        float x = sc[qb][r] * c2 - lse2[qb];
+        if (MASK && !valid(ko, qb)) x = -__builtin_huge_valf();
+        ds[kb][qb][r] = __builtin_amdgcn_exp2f(x) * (dp[qb][r] - dl[qb]);
       }
-      ds[kb][0][r] = __builtin_amdgcn_exp2f(x0) * (p0[r] - dl[0]);
-      ds[kb][1][r] = __builtin_amdgcn_exp2f(x1) * (p1[r] - dl[1]);
     }
   }
 #pragma unroll
   for (int kc = 0; kc < kKC; ++kc) {
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NB; ++qb) {
       const float v8[8] = {ds[2 * kc][qb][0],     ds[2 * kc][qb][1],     ds[2 * kc][qb][2],
                            ds[2 * kc][qb][3],     ds[2 * kc + 1][qb][0], ds[2 * kc + 1][qb][1],
                            ds[2 * kc + 1][qb][2], ds[2 * kc + 1][qb][3]};
@@ -154,15 +159,15 @@ __device__ __forceinline__ void dq_tile(const T* sK, const T* sV, const T* sKt,
 #pragma unroll
     for (int kc = 0; kc < kKC; ++kc) {
       const Frag<T> kt = lds_frag_2x4<T>(row + 32 * kc + 4 * g, row + 32 * kc + 16 + 4 * g);
-      dqa[db][0] = mma(dqa[db][0], kt, dsf[kc][0]);
-      dqa[db][1] = mma(dqa[db][1], kt, dsf[kc][1]);
+#pragma unroll
+      for (int qb = 0; qb < NB; ++qb) dqa[db][qb] = mma(dqa[db][qb], kt, dsf[kc][qb]);
     }
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int NB>
 __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
-  using Tr = BwdTraits<T, D>;
+  using Tr = BwdTraits<T, D, NB>;
   __shared__ __attribute__((aligned(16))) T sK[Tr::kBN * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sV[Tr::kBN * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sKt[D * Tr::kLDTN];
@@ -191,11 +196,11 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
   const T* gkp = static_cast<const T*>(a.gk) + gbase;
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
 
-  Frag<T> qf[2][Tr::kDC], df[2][Tr::kDC];
-  int qi[2];
-  float lse2[2], dl[2];
+  Frag<T> qf[NB][Tr::kDC], df[NB][Tr::kDC];
+  int qi[NB];
+  float lse2[NB], dl[NB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NB; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
     const bool ok = qi[qb] < S;
     lse2[qb] = ok ? lse[qi[qb]] * kLog2e : 0.f;
@@ -212,9 +217,11 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
     }
   }
   const float c2 = a.scale * kLog2e;
-  f32x4 dqa[Tr::kDB][2];
+  f32x4 dqa[Tr::kDB][NB];
 #pragma unroll
-  for (int db = 0; db < Tr::kDB; ++db) dqa[db][0] = dqa[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int db = 0; db < Tr::kDB; ++db)
+#pragma unroll
+    for (int qb = 0; qb < NB; ++qb) dqa[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const bool active = q0 < S;
   const int q_last = min(q0 + Tr::kQW, S) - 1;
@@ -238,16 +245,18 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
         return j <= qi[qb] && j >= qi[qb] - W + 1;
       };
       if (full)
-        dq_tile<T, D, false>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+        dq_tile<T, D, NB, false>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
       else
-        dq_tile<T, D, true>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+        dq_tile<T, D, NB, true>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
     }
   }
 
   const int gmax = glob_prefix(hi - 1, W, rpb);
   const int wg_lo = active ? glob_prefix(q0, W, rpb) : 0;
   const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
-  const int glen[2] = {glob_prefix(qi[0], W, rpb), glob_prefix(qi[1], W, rpb)};
+  int glen[NB];
+#pragma unroll
+  for (int qb = 0; qb < NB; ++qb) glen[qb] = glob_prefix(qi[qb], W, rpb);
   for (int ts = 0; ts < gmax; ts += Tr::kBN) {
     stk.load(gkp, D, ts, 0, gmax, tid);
     stv.load(gvp, D, ts, 0, gmax, tid);
@@ -259,15 +268,15 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
     if (active && ts < wg_hi) {
       auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
       if (ts + Tr::kBN <= wg_lo)
-        dq_tile<T, D, false>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+        dq_tile<T, D, NB, false>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
       else
-        dq_tile<T, D, true>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
+        dq_tile<T, D, NB, true>(sK, sV, sKt, qf, df, dqa, lse2, dl, c2, l16, g, valid);
     }
   }
 
   T* dqp = static_cast<T*>(a.dq) + b * a.dqsb + h * a.dqsh + (int64_t)dc.off * a.dqss;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NB; ++qb) {
     if (!active || qi[qb] >= S) continue;
     T* row = dqp + (int64_t)qi[qb] * a.dqss;
 #pragma unroll
@@ -280,31 +289,33 @@ __global__ __launch_bounds__(256) void dq_kernel(BwdArgs a) {
 // result is an fp32 partial per query chunk; LOC: the keys are rows of k/v,
 // the queries their local band, and the epilogue folds in the global rows.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool GLOB, bool MASK>
+template <typename T, int D, int NB, bool GLOB, bool MASK>
 __device__ __forceinline__ void dkdv_tile(const T* sQ, const T* sO, const T* sQt, const T* sOt,
                                           const float* sL, const float* sDl, const int* sGl,
-                                          const Frag<T> (&kf)[2][BwdTraits<T, D>::kDC],
-                                          const Frag<T> (&vf)[2][BwdTraits<T, D>::kDC],
-                                          f32x4 (&dka)[BwdTraits<T, D>::kDB][2],
-                                          f32x4 (&dva)[BwdTraits<T, D>::kDB][2], float c2,
+                                          const Frag<T> (&kf)[NB][BwdTraits<T, D, NB>::kDC],
+                                          const Frag<T> (&vf)[NB][BwdTraits<T, D, NB>::kDC],
+                                          f32x4 (&dka)[BwdTraits<T, D, NB>::kDB][NB],
+                                          f32x4 (&dva)[BwdTraits<T, D, NB>::kDB][NB], float c2,
                                           int l16, int g, int ts, int kw, int W, int q_hi) {
-  using Tr = BwdTraits<T, D>;
+  using Tr = BwdTraits<T, D, NB>;
   constexpr int kQS = Tr::kBQ / 32;  // 32-query steps per tile
 #pragma unroll
   for (int qs = 0; qs < kQS; ++qs) {
-    float p[2][2][4], ds[2][2][4];  // [query block][key block][r]
+    float p[2][NB][4], ds[2][NB][4];  // [query block][key block][r]
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int qo = 32 * qs + 16 * qb;
-      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, d0 = s0, d1 = s0;
+      f32x4 sc[NB], dd[NB];
+#pragma unroll
+      for (int kb = 0; kb < NB; ++kb) sc[kb] = dd[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < Tr::kDC; ++c) {
         const Frag<T> qa = lds_frag_row<T>(sQ + (qo + l16) * Tr::kLD + 32 * c + 8 * g);
         const Frag<T> oa = lds_frag_row<T>(sO + (qo + l16) * Tr::kLD + 32 * c + 8 * g);
-        s0 = mma(s0, qa, kf[0][c]);
-        s1 = mma(s1, qa, kf[1][c]);
-        d0 = mma(d0, oa, vf[0][c]);
-        d1 = mma(d1, oa, vf[1][c]);
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) sc[kb] = mma(sc[kb], qa, kf[kb][c]);
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) dd[kb] = mma(dd[kb], oa, vf[kb][c]);
       }
       const f32x4 lq = *reinterpret_cast<const f32x4*>(sL + qo + 4 * g);
       const f32x4 dq = *reinterpret_cast<const f32x4*>(sDl + qo + 4 * g);
@@ -316,29 +327,22 @@ __device__ __forceinline__ void dkdv_tile(const T* sQ, const T* sO, const T* sQt
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int qabs = ts + qo + 4 * g + r;
-        float x0 = s0[r] * c2 - lq[r];
-        float x1 = s1[r] * c2 - lq[r];
-        if (MASK) {
-          const int j0 = kw + l16, j1 = kw + 16 + l16;
-          bool v0, v1;
-          if (GLOB) {
-            v0 = qabs < q_hi && j0 < gq[r];
-            v1 = qabs < q_hi && j1 < gq[r];
-          } else {
-            v0 = qabs < q_hi && j0 <= qabs && j0 >= qabs - W + 1;
-            v1 = qabs < q_hi && j1 <= qabs && j1 >= qabs - W + 1;
+#pragma unroll
+        for (int kb = 0; kb < NB; ++kb) {
+          float x = sc[kb][r] * c2 - lq[r];
+          if (MASK) {
+            const int j = kw + 16 * kb + l16;
+            const bool vis = GLOB ? (qabs < q_hi && j < gq[r])
+                                  : (qabs < q_hi && j <= qabs && j >= qabs - W + 1);
+            if (!vis) x = -__builtin_huge_valf();
           }
-          if (!v0) x0 = -__builtin_huge_valf();
-          if (!v1) x1 = -__builtin_huge_valf();
+          p[qb][kb][r] = __builtin_amdgcn_exp2f(x);
+          ds[qb][kb][r] = p[qb][kb][r] * (dd[kb][r] - dq[r]);
         }
-        p[qb][0][r] = __builtin_amdgcn_exp2f(x0);
-        p[qb][1][r] = __builtin_amdgcn_exp2f(x1);
-        ds[qb][0][r] = p[qb][0][r] * (d0[r] - dq[r]);
-        ds[qb][1][r] = p[qb][1][r] * (d1[r] - dq[r]);
       }
     }
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NB; ++kb) {
       const float pv[8] = {p[0][kb][0], p[0][kb][1], p[0][kb][2], p[0][kb][3],
                            p[1][kb][0], p[1][kb][1], p[1][kb][2], p[1][kb][3]};
       const float dv8[8] = {ds[0][kb][0], ds[0][kb][1], ds[0][kb][2], ds[0][kb][3],
@@ -358,9 +362,9 @@ __device__ __forceinline__ void dkdv_tile(const T* sQ, const T* sO, const T* sQt
   }
 }
 
-template <typename T, int D, bool GLOB>
+template <typename T, int D, int NB, bool GLOB>
 __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
-  using Tr = BwdTraits<T, D>;
+  using Tr = BwdTraits<T, D, NB>;
   __shared__ __attribute__((aligned(16))) T sQ[Tr::kBQ * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sO[Tr::kBQ * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sQt[D * Tr::kLDTQ];
@@ -403,9 +407,9 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
   }
 
   // K^T, V^T as B operands: lane holds row kw + 16kb + l16, dims 32c + 8g ..
-  Frag<T> kf[2][Tr::kDC], vf[2][Tr::kDC];
+  Frag<T> kf[NB][Tr::kDC], vf[NB][Tr::kDC];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < NB; ++kb) {
     const int row = kw + 16 * kb + l16;
 #pragma unroll
     for (int c = 0; c < Tr::kDC; ++c) {
@@ -418,10 +422,11 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
       }
     }
   }
-  f32x4 dka[Tr::kDB][2], dva[Tr::kDB][2];
+  f32x4 dka[Tr::kDB][NB], dva[Tr::kDB][NB];
 #pragma unroll
   for (int db = 0; db < Tr::kDB; ++db)
-    dka[db][0] = dka[db][1] = dva[db][0] = dva[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) dka[db][kb] = dva[db][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Query range of the workgroup and of this wave.
   const bool active = kw < nrows;
@@ -479,11 +484,11 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
         else
           full = ts >= k_last && ts + Tr::kBQ - 1 - W + 1 <= kw && ts + Tr::kBQ <= q_hi;
         if (full)
-          dkdv_tile<T, D, GLOB, false>(sQ, sO, sQt, sOt, sL, sDl, sGl, kf, vf, dka, dva, c2, l16,
-                                       g, ts, kw, W, q_hi);
+          dkdv_tile<T, D, NB, GLOB, false>(sQ, sO, sQt, sOt, sL, sDl, sGl, kf, vf, dka, dva, c2,
+                                           l16, g, ts, kw, W, q_hi);
         else
-          dkdv_tile<T, D, GLOB, true>(sQ, sO, sQt, sOt, sL, sDl, sGl, kf, vf, dka, dva, c2, l16,
-                                      g, ts, kw, W, q_hi);
+          dkdv_tile<T, D, NB, GLOB, true>(sQ, sO, sQt, sOt, sL, sDl, sGl, kf, vf, dka, dva, c2,
+                                          l16, g, ts, kw, W, q_hi);
       }
     }
   }
@@ -492,7 +497,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
   if (GLOB) {
     float* part = a.gpart + (((int64_t)chunk * nbh + bhk) * a.G + dc.gofs) * 2 * D;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < NB; ++kb) {
       const int row = kw + 16 * kb + l16;
       if (row >= nrows) continue;
       float* pk = part + (int64_t)row * 2 * D;
@@ -508,7 +513,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(BwdArgs a) {
   T* dvp = static_cast<T*>(a.dv) + b * a.dvsb + hk * a.dvsh + (int64_t)dc.off * a.dvss;
   const float rsc = (relay && a.rscale) ? a.rscale[hk] : 1.f;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < NB; ++kb) {
     const int j = kw + 16 * kb + l16;
     if (j >= S) continue;
 #pragma unroll
@@ -1328,24 +1333,32 @@ constexpr int kDqWPE = 2;   // dQ waves per SIMD (register budget)
 constexpr int kDkdvGlobBQ = 128;
 constexpr int kDkdvLocalBQ = 32;
 
+// The gfx950-tiled kernels (dq2, dkdv2) serve fp16/bf16 up to D = 128; the
+// generic kernels serve fp32 and every dtype at D = 256.
+template <typename T, int D>
+constexpr bool kTiledBwd = sizeof(T) == 2 && D <= 128;
+template <int D>
+constexpr int kGenericNB = D > 128 ? 1 : 2;
+
 template <typename T, int D>
 hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
-  using Tr = BwdTraits<T, D>;
+  constexpr bool kTiled = kTiledBwd<T, D>;
+  constexpr int NB = kGenericNB<D>;
+  using Tr = BwdTraits<T, D, NB>;
   constexpr int kRows = 256 / (D / 8);
-  // fp16/bf16: dq2_kernel computes Delta for its own queries and stores -Delta
-  // (with -lse * log2(e)) for the dK/dV kernels
-  if (sizeof(T) == 4 && a.group == 0)
+  // tiled path: dq2_kernel computes Delta for its own queries and stores
+  // -Delta (with -lse * log2(e)) for the dK/dV kernels
+  if (!kTiled && a.group == 0)
     hipLaunchKernelGGL((delta_kernel<T, D>), dim3((a.S + kRows - 1) / kRows, a.B * a.Hq),
                        dim3(256), 0, st, a);
   // work items per document: query tiles (dQ), global-row tiles x query
   // chunks (global dK/dV), key tiles (local dK/dV), each of its kernel's
   // workgroup size
   BwdArgs aq = a, ag = a, al = a;
-  constexpr int kQM = sizeof(T) == 2 ? 16 * kDqWaves * kDqQB : Tr::kBM;  // dQ queries per workgroup
+  constexpr int kQM = kTiled ? 16 * kDqWaves * kDqQB : Tr::kBM;  // dQ queries per workgroup
   set_items(aq.docs, [&](int d) { return (a.docs.len[d] + kQM - 1) / kQM; });
-  constexpr bool kMfma = sizeof(T) == 2;
-  constexpr int kGK = kMfma ? 16 * kDkdvGlobWaves<D> * kDkdvKB : Tr::kBK;   // rows per workgroup
-  constexpr int kLK = kMfma ? 16 * kDkdvLocalWaves * kDkdvLocalKB<D> : Tr::kBK;
+  constexpr int kGK = kTiled ? 16 * kDkdvGlobWaves<D> * kDkdvKB : Tr::kBK;   // rows per workgroup
+  constexpr int kLK = kTiled ? 16 * kDkdvLocalWaves * kDkdvLocalKB<D> : Tr::kBK;
   set_items(ag.docs, [&](int d) {
     const int g = (a.docs.len[d] + a.docs.W[d] - 1) / a.docs.W[d] * a.docs.rpb[d];
     return (g + kGK - 1) / kGK * a.nchunk;
@@ -1353,14 +1366,15 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   set_items(al.docs, [&](int d) { return (a.docs.len[d] + kLK - 1) / kLK; });
   const int nq = aq.docs.item0[a.docs.n], ng = ag.docs.item0[a.docs.n];
   const int nl = al.docs.item0[a.docs.n];
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (kTiled) {
     hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, kDqQB, kDqBN, kDqWPE>), dim3(nq * a.B * a.Hq),
                        dim3(64 * kDqWaves), 0, st, aq);
     hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvGlobWaves<D>, kDkdvKB, kDkdvGlobBQ>),
                        dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvGlobWaves<D>), 0, st, ag);
   } else {
-    hipLaunchKernelGGL((dq_kernel<T, D>), dim3(nq * a.B * a.Hq), dim3(256), 0, st, aq);
-    hipLaunchKernelGGL((dkdv_kernel<T, D, true>), dim3(ng * a.B * a.Hkv), dim3(256), 0, st, ag);
+    hipLaunchKernelGGL((dq_kernel<T, D, NB>), dim3(nq * a.B * a.Hq), dim3(256), 0, st, aq);
+    hipLaunchKernelGGL((dkdv_kernel<T, D, NB, true>), dim3(ng * a.B * a.Hkv), dim3(256), 0, st,
+                       ag);
   }
   if (a.nchunk > 1) {
     BwdArgs as = a;
@@ -1372,11 +1386,12 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
                        0, st, as);
   }
   if (a.dalpha) hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
-  if constexpr (sizeof(T) == 2)
+  if constexpr (kTiled)
     hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvLocalWaves, kDkdvLocalKB<D>, kDkdvLocalBQ>),
                        dim3(nl * a.B * a.Hkv), dim3(64 * kDkdvLocalWaves), 0, st, al);
   else
-    hipLaunchKernelGGL((dkdv_kernel<T, D, false>), dim3(nl * a.B * a.Hkv), dim3(256), 0, st, al);
+    hipLaunchKernelGGL((dkdv_kernel<T, D, NB, false>), dim3(nl * a.B * a.Hkv), dim3(256), 0, st,
+                       al);
   return hipGetLastError();
 }
 
@@ -1386,6 +1401,7 @@ hipError_t launch_T(int D, const BwdArgs& a, hipStream_t st) {
     case 32: return launch_TD<T, 32>(a, st);
     case 64: return launch_TD<T, 64>(a, st);
     case 128: return launch_TD<T, 128>(a, st);
+    case 256: return launch_TD<T, 256>(a, st);
   }
   return hipErrorInvalidValue;
 }
@@ -1409,7 +1425,11 @@ size_t bwd_workspace_bytes(int D, int B, int Hq, int Hkv, int S, int n, const in
   //   B=1 H=12 D=64 S=8192 / 32768 / 131072: 22 / 13 / 22 chunks
   //   B=2 H=32 D=128 S=4096: 6 (the previous rule's 16 was 12% slower)
   //   B=1 H=8 D=64 S=16384: 32 (64 was 10% slower)
-  const int rows = D == 128 ? 16 * kDkdvGlobWaves<128> * kDkdvKB : 16 * kDkdvGlobWaves<64> * kDkdvKB;
+  // (D = 256 runs the generic global-row kernel: 64 rows per 4-wave
+  // workgroup, two workgroups per CU by their 71 KB of LDS)
+  const int rows = D > 128    ? BwdTraits<f16, 256, 1>::kBK
+                   : D == 128 ? 16 * kDkdvGlobWaves<128> * kDkdvKB
+                              : 16 * kDkdvGlobWaves<64> * kDkdvKB;
   const int slots = (cus > 0 ? cus : 256) * (D == 128 ? 1 : 2);
   int64_t row_tiles = 0;
   int max_len = 1;
@@ -1438,8 +1458,13 @@ size_t bwd_workspace_layout(int D, int B, int Hq, int Hkv, int S, int64_t G, int
 }
 
 bool bwd_tile_config(int dtype, int D, int out[9]) {
-  if (dtype < 0 || dtype > 2 || (D != 32 && D != 64 && D != 128)) return false;
-  if (dtype == 2) {
+  if (dtype < 0 || dtype > 2 || (D != 32 && D != 64 && D != 128 && D != 256)) return false;
+  if (D == 256) {
+    using Tr = BwdTraits<f16, 256, 1>;  // the same geometry for every dtype
+    const int waves = Tr::kThreads / 64;
+    const int v[9] = {waves, Tr::kBM, Tr::kBN, waves, Tr::kBK, Tr::kBQ, waves, Tr::kBK, Tr::kBQ};
+    for (int i = 0; i < 9; ++i) out[i] = v[i];
+  } else if (dtype == 2) {
     using Tr = BwdTraits<float, 128>;
     const int waves = Tr::kThreads / 64;
     const int v[9] = {waves, Tr::kBM, Tr::kBN, waves, Tr::kBK, Tr::kBQ, waves, Tr::kBK, Tr::kBQ};

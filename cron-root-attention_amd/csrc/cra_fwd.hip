@@ -31,13 +31,16 @@ namespace cra {
 
 namespace {
 
-template <typename T, int D>
+// Geometry of the generic forward (fwd_kernel: the fp32 path, and every
+// dtype at head dim 256). NB = 16-query blocks per wave: two below D = 256,
+// one at D = 256 (two would hold 256 VGPRs of accumulators and Q operands).
+template <typename T, int D, int NB = 2>
 struct FwdTraits {
   static constexpr int kWaves = 4;
   static constexpr int kThreads = 64 * kWaves;
-  static constexpr int kQW = 32;                     // queries per wave
+  static constexpr int kQW = 16 * NB;                // queries per wave
   static constexpr int kBM = kWaves * kQW;           // queries per workgroup
-  static constexpr int kBN = sizeof(T) == 4 ? 32 : 64;  // key rows per LDS tile
+  static constexpr int kBN = (sizeof(T) == 4 || D > 128) ? 32 : 64;  // key rows per LDS tile
   static constexpr int kKB = kBN / 16;               // 16-row key blocks
   static constexpr int kKC = kBN / 32;               // 32-row key chunks
   static constexpr int kDC = D / 32;                 // 32-wide head-dim chunks
@@ -46,31 +49,31 @@ struct FwdTraits {
   static constexpr int kLDT = kBN + 4;               // transposed tile stride
 };
 
-// One key tile against the wave's 32 queries: S^T, masked online softmax,
-// O^T += V^T P^T. `valid(key_offset, qb)` says whether tile row key_offset is
-// in the set of query block qb's lane query.
-template <typename T, int D, bool MASK, typename Valid>
+// One key tile against the wave's 16 * NB queries: S^T, masked online
+// softmax, O^T += V^T P^T. `valid(key_offset, qb)` says whether tile row
+// key_offset is in the set of query block qb's lane query.
+template <typename T, int D, int NB, bool MASK, typename Valid>
 __device__ __forceinline__ void attend_tile(const T* sK, const T* sVt,
-                                            const Frag<T> (&qf)[2][FwdTraits<T, D>::kDC],
-                                            f32x4 (&acc)[FwdTraits<T, D>::kDB][2],
-                                            float (&m_run)[2], float (&l_run)[2], float c2,
+                                            const Frag<T> (&qf)[NB][FwdTraits<T, D, NB>::kDC],
+                                            f32x4 (&acc)[FwdTraits<T, D, NB>::kDB][NB],
+                                            float (&m_run)[NB], float (&l_run)[NB], float c2,
                                             int l16, int g, Valid valid) {
-  using Tr = FwdTraits<T, D>;
-  f32x4 s[Tr::kKB][2];
+  using Tr = FwdTraits<T, D, NB>;
+  f32x4 s[Tr::kKB][NB];
 #pragma unroll
   for (int kb = 0; kb < Tr::kKB; ++kb) {
-    s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int qb = 0; qb < NB; ++qb) s[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < Tr::kDC; ++c) {
       const Frag<T> kf = lds_frag_row<T>(sK + (16 * kb + l16) * Tr::kLD + 32 * c + 8 * g);
-      s[kb][0] = mma(s[kb][0], kf, qf[0][c]);
-      s[kb][1] = mma(s[kb][1], kf, qf[1][c]);
+#pragma unroll
+      for (int qb = 0; qb < NB; ++qb) s[kb][qb] = mma(s[kb][qb], kf, qf[qb][c]);
     }
   }
-  Frag<T> pf[Tr::kKC][2];
+  Frag<T> pf[Tr::kKC][NB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NB; ++qb) {
     float t[Tr::kKB][4];
     float mx = -__builtin_huge_valf();
 #pragma unroll
@@ -114,15 +117,18 @@ __device__ __forceinline__ void attend_tile(const T* sK, const T* sVt,
 #pragma unroll
     for (int kc = 0; kc < Tr::kKC; ++kc) {
       const Frag<T> vf = lds_frag_2x4<T>(row + 32 * kc + 4 * g, row + 32 * kc + 16 + 4 * g);
-      acc[db][0] = mma(acc[db][0], vf, pf[kc][0]);
-      acc[db][1] = mma(acc[db][1], vf, pf[kc][1]);
+#pragma unroll
+      for (int qb = 0; qb < NB; ++qb) acc[db][qb] = mma(acc[db][qb], vf, pf[kc][qb]);
     }
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
-  using Tr = FwdTraits<T, D>;
+// At D = 256 the 2-byte forward fits 2 waves per SIMD (at most 256 VGPRs).
+template <typename T, int D, int NB>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(D > 128 && sizeof(T) == 2 ? 2 : 1)))
+void fwd_kernel(FwdArgs a) {
+  using Tr = FwdTraits<T, D, NB>;
   __shared__ __attribute__((aligned(16))) T sK[Tr::kBN * Tr::kLD];
   __shared__ __attribute__((aligned(16))) T sVt[D * Tr::kLDT];
 
@@ -148,10 +154,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   const T* gvp = static_cast<const T*>(a.gv) + gbase;
 
   // Q as the B operand of S^T = K . Q^T: lane holds q[qi][32c + 8g .. +8].
-  Frag<T> qf[2][Tr::kDC];
-  int qi[2];
+  Frag<T> qf[NB][Tr::kDC];
+  int qi[NB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NB; ++qb) {
     qi[qb] = q0 + 16 * qb + l16;
 #pragma unroll
     for (int c = 0; c < Tr::kDC; ++c) {
@@ -165,11 +171,15 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   }
 
   const float c2 = a.scale * kLog2e;
-  float m_run[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};
-  float l_run[2] = {0.f, 0.f};
-  f32x4 acc[Tr::kDB][2];
+  float m_run[NB], l_run[NB];
+  f32x4 acc[Tr::kDB][NB];
 #pragma unroll
-  for (int db = 0; db < Tr::kDB; ++db) acc[db][0] = acc[db][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qb = 0; qb < NB; ++qb) {
+    m_run[qb] = -__builtin_huge_valf();
+    l_run[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < Tr::kDB; ++db) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   const bool active = q0 < S;
   const int q_last = min(q0 + Tr::kQW, S) - 1;
@@ -194,9 +204,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
         return j <= qi[qb] && j >= qi[qb] - W + 1;
       };
       if (full)
-        attend_tile<T, D, false>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+        attend_tile<T, D, NB, false>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
       else
-        attend_tile<T, D, true>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+        attend_tile<T, D, NB, true>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
     }
   }
 
@@ -204,7 +214,9 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
   const int gmax = glob_prefix(hi - 1, W, rpb);
   const int wg_lo = active ? glob_prefix(q0, W, rpb) : 0;
   const int wg_hi = active ? glob_prefix(q_last, W, rpb) : 0;
-  const int glen[2] = {glob_prefix(qi[0], W, rpb), glob_prefix(qi[1], W, rpb)};
+  int glen[NB];
+#pragma unroll
+  for (int qb = 0; qb < NB; ++qb) glen[qb] = glob_prefix(qi[qb], W, rpb);
   const int g_end = (a.phases & 2) ? gmax : 0;
   for (int ts = 0; ts < g_end; ts += Tr::kBN) {
     stk.load(gkp, D, ts, 0, gmax, tid);
@@ -216,16 +228,16 @@ __global__ __launch_bounds__(256) void fwd_kernel(FwdArgs a) {
     if (active && ts < wg_hi) {
       auto valid = [&](int ko, int qb) { return ts + ko < glen[qb]; };
       if (ts + Tr::kBN <= wg_lo)
-        attend_tile<T, D, false>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+        attend_tile<T, D, NB, false>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
       else
-        attend_tile<T, D, true>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
+        attend_tile<T, D, NB, true>(sK, sVt, qf, acc, m_run, l_run, c2, l16, g, valid);
     }
   }
 
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) ln 2 ---------------------
   T* op = static_cast<T*>(a.o) + b * a.osb + h * a.osh + (int64_t)dc.off * a.oss;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NB; ++qb) {
     const float l = group_sum(l_run[qb]);
     if (!active || qi[qb] >= S) continue;
     const float inv = 1.f / fmaxf(l, 1e-6f);
@@ -698,8 +710,23 @@ hipError_t resident_slots(K kern, int threads, int* out) {
 // measured 4% slower at D = 128: the wider local window adds key tiles.
 constexpr int kFwdWaves = 4;
 
+// Head dim 256, every dtype: the generic forward with 16 queries per wave
+// (64 per workgroup). A persistent request runs the same tiled kernel (the
+// work-queue form is built for the gfx950-tiled kernel only; the results
+// are the same function of the inputs).
+template <typename T>
+hipError_t launch_wide(const FwdArgs& a, hipStream_t st) {
+  using Tr = FwdTraits<T, 256, 1>;
+  FwdArgs b = a;
+  set_items(b.docs, [&](int d) { return (b.docs.len[d] + Tr::kBM - 1) / Tr::kBM; });
+  const dim3 grid(b.docs.item0[b.docs.n] * b.B * b.Hq);
+  hipLaunchKernelGGL((fwd_kernel<T, 256, 1>), grid, dim3(Tr::kThreads), 0, st, b);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
+  if (D == 256) return launch_wide<T>(a, st);
   if constexpr (sizeof(T) == 2) {
     FwdArgs b = a;
     constexpr int kBM = 32 * kFwdWaves;
@@ -734,12 +761,13 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
     if (qerr != hipSuccess) return qerr;
   } else {
     FwdArgs b = a;
-    set_items(b.docs, [&](int d) { return (b.docs.len[d] + 127) / 128; });
+    constexpr int kBM = FwdTraits<T, 128, 2>::kBM;
+    set_items(b.docs, [&](int d) { return (b.docs.len[d] + kBM - 1) / kBM; });
     const dim3 grid(b.docs.item0[b.docs.n] * b.B * b.Hq);
     switch (D) {
-      case 32: hipLaunchKernelGGL((fwd_kernel<T, 32>), grid, dim3(256), 0, st, b); break;
-      case 64: hipLaunchKernelGGL((fwd_kernel<T, 64>), grid, dim3(256), 0, st, b); break;
-      case 128: hipLaunchKernelGGL((fwd_kernel<T, 128>), grid, dim3(256), 0, st, b); break;
+      case 32: hipLaunchKernelGGL((fwd_kernel<T, 32, 2>), grid, dim3(256), 0, st, b); break;
+      case 64: hipLaunchKernelGGL((fwd_kernel<T, 64, 2>), grid, dim3(256), 0, st, b); break;
+      case 128: hipLaunchKernelGGL((fwd_kernel<T, 128, 2>), grid, dim3(256), 0, st, b); break;
       default: return hipErrorInvalidValue;
     }
   }
@@ -750,8 +778,11 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
 
 
 bool fwd_tile_config(int dtype, int D, int out[3]) {
-  if (dtype < 0 || dtype > 2 || (D != 32 && D != 64 && D != 128)) return false;
-  if (dtype == 2) {
+  if (dtype < 0 || dtype > 2 || (D != 32 && D != 64 && D != 128 && D != 256)) return false;
+  if (D == 256) {
+    using Tr = FwdTraits<f16, 256, 1>;  // the same geometry for every dtype
+    out[0] = Tr::kWaves; out[1] = Tr::kBM; out[2] = Tr::kBN;
+  } else if (dtype == 2) {
     using Tr = FwdTraits<float, 128>;
     out[0] = Tr::kWaves; out[1] = Tr::kBM; out[2] = Tr::kBN;
   } else {

@@ -198,6 +198,7 @@ hipError_t launch_T(int D, const GlobalArgs& args, int B, hipStream_t st) {
     case 32: hipLaunchKernelGGL((build_global_kernel<T, 32>), grid, dim3(256), 0, st, a); break;
     case 64: hipLaunchKernelGGL((build_global_kernel<T, 64>), grid, dim3(256), 0, st, a); break;
     case 128: hipLaunchKernelGGL((build_global_kernel<T, 128>), grid, dim3(256), 0, st, a); break;
+    case 256: hipLaunchKernelGGL((build_global_kernel<T, 256>), grid, dim3(256), 0, st, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

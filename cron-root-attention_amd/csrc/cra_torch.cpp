@@ -2,7 +2,7 @@
 // in C++: torch.ops.cra.attention(q, k, v, window, relay, top_k, scale).
 //
 // It serves the common call of cron_root_attention_v14 (reference
-// core.py:3767-3797) -- GPU tensors, head dim 32/64/128, no
+// core.py:3767-3797) -- GPU tensors, head dim 32/64/128/256, no
 // relay_log_scale, the tiled forward -- with the
 // same launches as the Python autograd Function (cra_build_global + cra_fwd,
 // then cra_bwd) but without the Python autograd and ctypes layers, which at
@@ -170,7 +170,8 @@ void check_inputs(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v)
   TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
               "cra::attention: q, k, v dtypes differ");
   const int64_t D = q.size(3);
-  TORCH_CHECK(D == 32 || D == 64 || D == 128, "cra::attention: head dim must be 32, 64 or 128");
+  TORCH_CHECK(D == 32 || D == 64 || D == 128 || D == 256,
+              "cra::attention: head dim must be 32, 64, 128 or 256");
 }
 
 // The tensor itself when the kernels take its layout, else a contiguous copy

@@ -70,7 +70,8 @@ typedef struct {
   char device_name[128];
 } cra_device_info_t;
 
-/* Head dims the kernels are built for (others: pad to one of them). */
+/* Head dims the kernels are built for: 32, 64, 128 and 256 (others up to
+ * 256: pad to the next one; the reference takes any D, core.py:3495). */
 int cra_supported_head_dim(int32_t D);
 
 /* Rows of the packed "global" key/value array per (b, kv head):

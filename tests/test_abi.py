@@ -39,7 +39,7 @@ def test_strerror_covers_codes():
 
 def test_supported_head_dims():
     lib = N.load_library()
-    assert [d for d in range(1, 300) if lib.cra_supported_head_dim(d)] == [32, 64, 128]
+    assert [d for d in range(1, 600) if lib.cra_supported_head_dim(d)] == [32, 64, 128, 256]
 
 
 def prob(**kw):
@@ -271,10 +271,15 @@ def test_tile_config_reports_compiled_geometry():
     built; a workgroup's rows are waves x rows per wave."""
     import torch
     for dt in (torch.float16, torch.bfloat16, torch.float32):
-        for D in (32, 64, 128):
+        for D in (32, 64, 128, 256):
             t = N.tile_config(dt, D)
             assert all(v > 0 for v in t.values())
-            assert t["fwd_queries"] == 32 * t["fwd_waves"]
+            # 32 queries per wave; 16 at D = 256 (the generic kernels' register budget)
+            assert t["fwd_queries"] == (16 if D == 256 else 32) * t["fwd_waves"]
+    h256 = N.tile_config(torch.bfloat16, 256)
+    assert (h256["fwd_waves"], h256["fwd_queries"], h256["fwd_key_tile"]) == (4, 64, 32)
+    assert (h256["dq_queries"], h256["dkdv_global_rows"], h256["dkdv_local_keys"]) == (64, 64, 64)
+    assert lib_tc_unsupported(512)
     h = N.tile_config(torch.float16, 128)
     assert (h["fwd_waves"], h["fwd_queries"], h["fwd_key_tile"]) == (4, 128, 64)
     assert (h["dkdv_global_waves"], h["dkdv_global_rows"]) == (12, 192)
@@ -290,6 +295,14 @@ def test_tile_config_reports_compiled_geometry():
     import cron_root_attention as cra
     cfg = cra.calibrate(16, 128, verbose=False)
     assert cfg == {"fwd": (h["fwd_waves"], 2), "bwd": (h["dq_waves"], 2)}   # reference's keys
+    # the generic kernels (fp32, D = 256) stage one tile at a time
+    assert cra.calibrate(16, 200, dtype=torch.float16, verbose=False) == {"fwd": (4, 1),
+                                                                          "bwd": (4, 1)}
+
+
+def lib_tc_unsupported(D):
+    out = N.CraTileConfig()
+    return N.load_library().cra_tile_config(0, D, ctypes.byref(out)) == N.E_UNSUPPORTED
 
 
 def test_fwd_persistent_requires_a_counter():

@@ -89,9 +89,10 @@ def test_module_hybrid_flag_routes_short_sequences_to_sdpa():
 
 def test_head_dim_limit():
     from cron_root_attention.core import _padded_head_dim
-    assert [_padded_head_dim(d) for d in (1, 16, 32, 33, 64, 65, 128)] == [32, 32, 32, 64, 64, 128, 128]
+    assert ([_padded_head_dim(d) for d in (1, 16, 32, 33, 64, 65, 128, 129, 200, 256)]
+            == [32, 32, 32, 64, 64, 128, 128, 256, 256, 256])
     with pytest.raises(NotImplementedError):
-        _padded_head_dim(129)
+        _padded_head_dim(257)
 
 
 def test_gpu_info_without_gpu():

@@ -33,6 +33,7 @@ CASES = [
     (1, 2, 1, 2500, 64, torch.float32, "bhsd"),     # fp32 kernels, GQA 2:1
     (1, 3, 3, 1, 128, torch.float16, "bhsd"),       # a single query
     (1, 2, 2, 2300, 64, torch.float16, "bhds"),     # copied layout
+    (1, 4, 2, 3000, 256, torch.bfloat16, "bhsd"),   # head dim 256 (generic kernels), GQA
 ]
 
 

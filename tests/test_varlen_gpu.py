@@ -101,6 +101,7 @@ FWD_CASES = [
     (BF16, 2, 4, 2, 64, [3000, 63, 2049, 300]),
     (F32, 1, 2, 1, 32, [100, 2100, 17]),
     (F16, 1, 4, 4, 96, [128, 2300, 999]),
+    (BF16, 1, 2, 2, 256, [900, 2100, 33]),     # head dim 256 (generic kernels)
 ]
 
 
@@ -137,6 +138,7 @@ BWD_CASES = [
     (F16, 1, 2, 2, 128, [700, 1, 2500, 65]),
     (BF16, 1, 4, 2, 64, [2049, 300, 64, 1000]),
     (F32, 2, 2, 1, 32, [100, 2100, 17]),
+    (F16, 1, 2, 1, 256, [1500, 2200, 40]),     # head dim 256 (generic kernels)
 ]
 
 
