@@ -44,6 +44,9 @@ sys.path.insert(0, ROOT)
 METRIC = "fwd & fwd+bwd ms + eff. TFLOP/s, H=16 D=128 S=128K fp16, 1 MI355X"
 PEAK_FP16_TFLOPS = 2500.0      # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0
+MFMA_FLOPS = 2 * 16 * 16 * 32   # one v_mfma_f32_16x16x32_{f16,bf16}
+CUS = 256                       # MI355X compute units (4 SIMDs each)
+TARGET_FRAC = 0.5               # the north star's roofline fraction
 
 
 def pairs_fast(S: int, top_k: int = 2) -> int:
@@ -202,12 +205,93 @@ def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
     return out
 
 
+def executed_for(workload: str):
+    """Executed MFMA instructions per kernel launch (SQ_INSTS_MFMA) and the
+    sustained clock, from the committed counter summary of this workload
+    (profiles/executed_<workload>.json, written by --counter-summary
+    --json-out from rocprofv3 --pmc passes over --profile-workload)."""
+    path = os.path.join(ROOT, "profiles", f"executed_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
 def traffic_for(kernel: str, workload: str):
     path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f).get("hbm_bytes_per_launch")
+
+
+def forward_phases(B, H, S, D, q, k, v, p, gk, gv, args, torch):
+    """Per-phase forward (cra_fwd_phases: the local window alone, the global
+    rows alone, and the global rows of a relay-off packing = the strided rows
+    alone) and the global-row build (K1, HBM-bound), each timed per launch.
+    The relay rows sit in the same packed tiles as the strided rows, so no
+    launch computes them alone: their share is reported as the difference of
+    the two global launches and labelled so. Counter-backed MFMA-busy shares
+    of the same launches come from profiles/phases_counters_<workload>.json
+    when present."""
+    from cron_root_attention import _native
+    dtype = q.dtype
+    W = int(math.ceil(math.sqrt(S)))
+    pp = phase_pairs(S)
+    t_loc = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_LOCAL),
+                          args.steps, args.warmup, torch)
+    t_glob = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv,
+                                                   phases=_native.PHASE_GLOBAL),
+                           args.steps, args.warmup, torch)
+    # strided rows alone: the same global-phase kernel over packed rows built
+    # without relay (one row per block); the relay rows' share is the
+    # difference to the full global phase
+    p_s = _native.problem(B, H, H, S, D, W, False, 2, dtype, 1 / math.sqrt(D))
+    gk_s, gv_s, _ = _native.build_global(p_s, k, v, None)
+    t_str = per_launch_ms(lambda: _native.forward(p_s, q, k, v, gk_s, gv_s,
+                                                  phases=_native.PHASE_GLOBAL),
+                          args.steps, args.warmup, torch)
+    del gk_s, gv_s
+    t_bg = per_launch_ms(lambda: _native.build_global(p, k, v, None), args.steps, args.warmup,
+                         torch)
+    G = int(_native.global_rows(p))
+    NB = (S + W - 1) // W
+    e = 2
+    bg_bytes = B * H * (S * D * e + G * D * e + 2 * G * D * e + 4 * NB * 2)
+    f_loc = 4 * D * pp["local"] * B * H
+    f_glob = 4 * D * (pp["strided"] + pp["relay"]) * B * H
+    f_str = 4 * D * pp["strided"] * B * H
+    t_rel = t_glob - t_str
+    phases = {
+        "local": {"ms": round(t_loc, 4), "pairs_per_head": pp["local"],
+                  "tflops": round(f_loc / (t_loc * 1e-3) / 1e12, 2),
+                  "mfma_frac": round(f_loc / (t_loc * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
+        "global": {"ms": round(t_glob, 4),
+                   "pairs_per_head": pp["strided"] + pp["relay"],
+                   "strided_pairs_per_head": pp["strided"], "relay_pairs_per_head": pp["relay"],
+                   "tflops": round(f_glob / (t_glob * 1e-3) / 1e12, 2),
+                   "mfma_frac": round(f_glob / (t_glob * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
+        "strided": {"ms": round(t_str, 4), "pairs_per_head": pp["strided"],
+                    "tflops": round(f_str / (t_str * 1e-3) / 1e12, 2),
+                    "mfma_frac": round(f_str / (t_str * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                    "how": "global phase over strided rows only (relay off)"},
+        "relay": {"ms_difference": round(t_rel, 4), "pairs_per_head": pp["relay"],
+                  "how": "global launch minus the strided-only launch: relay rows share the "
+                         "packed tiles of the strided rows, no launch computes them alone"},
+        "build_global": {"ms": round(t_bg, 4), "bytes": bg_bytes,
+                         "GBps": round(bg_bytes / (t_bg * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(bg_bytes / (t_bg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+    }
+    wl = f"H{H}_D{D}_S{S}_fp16"
+    cpath = os.path.join(ROOT, "profiles", f"phases_counters_{wl}.json")
+    if os.path.exists(cpath):
+        with open(cpath) as f:
+            cnt = json.load(f)
+        for name in ("local", "global", "strided"):
+            if name in cnt:
+                phases[name]["mfma_busy_counter"] = cnt[name]
+        phases["counters_source"] = "profiles/" + os.path.basename(cpath)
+    return phases
 
 
 def run_main(args):
@@ -249,55 +333,29 @@ def run_main(args):
             "traffic": traffic_for("fwd", workload), "avg_ms": round(kern_ms, 4),
             "algorithmic_flops": f_fwd}
 
-    # per-phase forward (cra_fwd_phases) and the global-row build (K1)
-    pp = phase_pairs(S)
-    t_loc = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_LOCAL),
-                          args.steps, args.warmup, torch)
-    t_glob = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv,
-                                                   phases=_native.PHASE_GLOBAL),
-                           args.steps, args.warmup, torch)
-    # strided rows alone: the same global-phase kernel over packed rows built
-    # without relay (one row per block); the relay rows' share is the
-    # difference to the full global phase
-    p_s = _native.problem(B, H, H, S, D, W, False, 2, dtype, 1 / math.sqrt(D))
-    gk_s, gv_s, _ = _native.build_global(p_s, k, v, None)
-    t_str = per_launch_ms(lambda: _native.forward(p_s, q, k, v, gk_s, gv_s,
-                                                  phases=_native.PHASE_GLOBAL),
-                          args.steps, args.warmup, torch)
-    del gk_s, gv_s
-    t_bg = per_launch_ms(lambda: _native.build_global(p, k, v, None), args.steps, args.warmup,
-                         torch)
-    G = int(_native.global_rows(p))
-    NB = (S + W - 1) // W
-    e = 2
-    bg_bytes = B * H * (S * D * e + G * D * e + 2 * G * D * e + 4 * NB * 2)
-    f_loc = 4 * D * pp["local"] * B * H
-    f_glob = 4 * D * (pp["strided"] + pp["relay"]) * B * H
-    f_str = 4 * D * pp["strided"] * B * H
-    f_rel = 4 * D * pp["relay"] * B * H
-    t_rel = t_glob - t_str
-    phases = {
-        "local": {"ms": round(t_loc, 4), "pairs_per_head": pp["local"],
-                  "tflops": round(f_loc / (t_loc * 1e-3) / 1e12, 2),
-                  "mfma_frac": round(f_loc / (t_loc * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
-        "global": {"ms": round(t_glob, 4),
-                   "pairs_per_head": pp["strided"] + pp["relay"],
-                   "strided_pairs_per_head": pp["strided"], "relay_pairs_per_head": pp["relay"],
-                   "tflops": round(f_glob / (t_glob * 1e-3) / 1e12, 2),
-                   "mfma_frac": round(f_glob / (t_glob * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)},
-        "strided": {"ms": round(t_str, 4), "pairs_per_head": pp["strided"],
-                    "tflops": round(f_str / (t_str * 1e-3) / 1e12, 2),
-                    "mfma_frac": round(f_str / (t_str * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
-                    "how": "global phase over strided rows only (relay off)"},
-        "relay": {"ms": round(t_rel, 4), "pairs_per_head": pp["relay"],
-                  "tflops": round(f_rel / (t_rel * 1e-3) / 1e12, 2) if t_rel > 0 else None,
-                  "mfma_frac": (round(f_rel / (t_rel * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
-                                if t_rel > 0 else None),
-                  "how": "global phase minus strided-only"},
-        "build_global": {"ms": round(t_bg, 4), "bytes": bg_bytes,
-                         "GBps": round(bg_bytes / (t_bg * 1e-3) / 1e9, 1),
-                         "hbm_frac": round(bg_bytes / (t_bg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
-    }
+    phases = forward_phases(B, H, S, D, q, k, v, p, gk, gv, args, torch)
+
+    # forward+backward against the same peak, with the executed MFMA work of
+    # the kernels (counter summary) beside the algorithmic 14*D*pairs
+    ex = executed_for(workload)
+    roof_fb = {"bound": "mfma", "achieved": round(f_all / (step_ms * 1e-3) / 1e12, 2),
+               "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(f_all / (step_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+               "algorithmic_flops": f_all, "ms": round(step_ms, 4)}
+    if ex:
+        n_mfma = sum(ex["mfma_per_launch"].values())
+        flops_ex = n_mfma * MFMA_FLOPS
+        roof_fb.update({
+            "executed_mfma": n_mfma, "executed_flops": flops_ex,
+            "executed_vs_algorithmic": round(flops_ex / f_all, 4),
+            "executed_frac": round(flops_ex / (step_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+            # MFMA-busy share every SIMD would need for half the nominal
+            # peak, at the clock these kernels sustain (counter summary)
+            "mfma_busy_needed_for_half_peak": round(
+                n_mfma * 16 / (TARGET_FRAC * f_all / (PEAK_FP16_TFLOPS * 1e12)
+                               * ex["clock_ghz"] * 1e9 * CUS * 4), 4),
+            "clock_ghz": ex["clock_ghz"], "per_kernel": ex["mfma_per_launch"],
+            "source": "profiles/executed_" + workload + ".json"})
 
     cpu = None
     if not args.skip_cpu:
@@ -314,9 +372,38 @@ def run_main(args):
         "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(f_fwd / (fwd_ms * 1e-3) / 1e12, 3),
         "fwdbwd_ms": round(step_ms, 4), "fwdbwd_tflops": round(f_all / (step_ms * 1e-3) / 1e12, 3),
         "pairs_per_head": P, "fwdbwd_per_step": spread(per_step),
-        "roofline": roof, "phases": phases, "cpu_baseline": cpu,
+        "roofline": roof, "roofline_fwdbwd": roof_fb, "phases": phases, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def run_phases(args):
+    """BASELINE config 3 (B=1 H=16 D=128 fp16) at each S of --phases: the
+    forward kernel's time and roofline fraction and the per-phase figures of
+    forward_phases, one JSON line per S."""
+    import torch
+    from cron_root_attention import _native
+    dev = torch.device("cuda", 0)
+    B, H, D = 1, 16, 128
+    for S in (int(x) for x in args.phases.split(",")):
+        gen = torch.Generator(device=dev).manual_seed(0)
+        q, k, v = (torch.randn(B, H, S, D, generator=gen, device=dev, dtype=torch.float32).half()
+                   for _ in range(3))
+        W = int(math.ceil(math.sqrt(S)))
+        p = _native.problem(B, H, H, S, D, W, S > 2048, 2, torch.float16, 1 / math.sqrt(D))
+        gk, gv, _ = _native.build_global(p, k, v, None)
+        kern_ms = per_launch_ms(lambda: _native.forward(p, q, k, v, gk, gv), args.steps,
+                                args.warmup, torch)
+        f_fwd = 4 * D * pairs_fast(S) * B * H
+        roof, bound, _ = roofline_ms(B, H, S, D, 2, False)
+        out = {"config": 3, "B": B, "H": H, "D": D, "S": S, "window": W,
+               "fwd_kernel_ms": round(kern_ms, 4),
+               "fwd_kernel_tflops": round(f_fwd / (kern_ms * 1e-3) / 1e12, 2),
+               "fwd_roofline_frac": round(roof / kern_ms, 4), "bound": bound,
+               "phases": forward_phases(B, H, S, D, q, k, v, p, gk, gv, args, torch)}
+        print(json.dumps(out), flush=True)
+        del q, k, v, gk, gv
+        torch.cuda.empty_cache()
 
 
 # BASELINE configurations 2-5 (config 1 is the CPU reference's plumbing case):
@@ -412,10 +499,15 @@ def run_configs(args):
 def run_profile_workload(args):
     """Short fixed workload for counter passes (rocprofv3 --pmc): a 1 GiB
     device copy first (read 1 GiB + write 1 GiB, the calibration of
-    FETCH_SIZE / WRITE_SIZE), then the hot path's kernels: build_global and
-    cra_fwd twice each, the local-only and global-only forwards once each,
-    then one backward."""
+    FETCH_SIZE / WRITE_SIZE), then the hot path's kernels at the shape
+    --pw B,H,S,D (default the north star, 1,16,131072,128; fp16):
+      mode "all":   build_global and cra_fwd twice each, the local-only, the
+                    global-only and the strided-only (relay-off packing)
+                    forwards once each, then one backward;
+      mode "train": one training step of the public op (forward + backward);
+      mode "fwd":   one forward of the public op."""
     import torch
+    import cron_root_attention as cra
     from cron_root_attention import _native
     dev = torch.device("cuda", 0)
     x = torch.empty(512 * 1024 * 1024, dtype=torch.float16, device=dev).fill_(1.0)
@@ -424,21 +516,34 @@ def run_profile_workload(args):
     y.copy_(x)
     torch.cuda.synchronize()
     del x, y
-    B, H, S, D = 1, 16, 131072, 128
+    B, H, S, D = (int(t) for t in args.pw.split(","))
     gen = torch.Generator(device=dev).manual_seed(0)
     q, k, v, do = (torch.randn(B, H, S, D, generator=gen, device=dev, dtype=torch.float32).half()
                    for _ in range(4))
     W = int(math.ceil(math.sqrt(S)))
-    p = _native.problem(B, H, H, S, D, W, True, 2, torch.float16, 1 / math.sqrt(D))
-    for _ in range(2):
-        gk, gv, src = _native.build_global(p, k, v, None)
-        o, lse = _native.forward(p, q, k, v, gk, gv)
-    # the local-window and global-row phases on their own (their own kernels)
-    _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_LOCAL)
-    _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_GLOBAL)
-    _native.backward(p, q, k, v, o, do, lse, gk, gv, src, None, False)
+    relay = S > 2048
+    if args.pw_mode == "all":
+        p = _native.problem(B, H, H, S, D, W, relay, 2, torch.float16, 1 / math.sqrt(D))
+        for _ in range(2):
+            gk, gv, src = _native.build_global(p, k, v, None)
+            o, lse = _native.forward(p, q, k, v, gk, gv)
+        # the local-window and global-row phases on their own (their own kernels),
+        # then the global phase over a relay-off packing (the strided rows alone)
+        _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_LOCAL)
+        _native.forward(p, q, k, v, gk, gv, phases=_native.PHASE_GLOBAL)
+        p_s = _native.problem(B, H, H, S, D, W, False, 2, torch.float16, 1 / math.sqrt(D))
+        gk_s, gv_s, _ = _native.build_global(p_s, k, v, None)
+        _native.forward(p_s, q, k, v, gk_s, gv_s, phases=_native.PHASE_GLOBAL)
+        _native.backward(p, q, k, v, o, do, lse, gk, gv, src, None, False)
+    elif args.pw_mode == "train":
+        qg, kg, vg = (t.requires_grad_(True) for t in (q, k, v))
+        cra.cron_root_attention(qg, kg, vg).backward(do)
+    else:
+        with torch.no_grad():
+            cra.cron_root_attention(q, k, v)
     torch.cuda.synchronize()
-    print(json.dumps({"profile_workload": "done", "B": B, "H": H, "S": S, "D": D}), flush=True)
+    print(json.dumps({"profile_workload": "done", "mode": args.pw_mode, "B": B, "H": H, "S": S,
+                      "D": D}), flush=True)
 
 
 def _demangle(name: str) -> str:
@@ -542,6 +647,77 @@ def counter_summary(dirs, cus: int = 256, xcds: int = 8):
     return "\n".join(lines) + "\n" + cal + "\n".join(extra) + "\n"
 
 
+def counter_dispatches(dirs):
+    """Per-dispatch counter records of rocprofv3 --pmc output directories, in
+    dispatch order: [(kernel, {counter: value}, duration_ns)] per pass."""
+    import csv
+    import glob
+    from collections import defaultdict
+    passes = []
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+            per = defaultdict(lambda: defaultdict(float))
+            meta = {}
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    per[int(r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
+                    meta[int(r["Dispatch_Id"])] = (_short_kernel(r["Kernel_Name"]),
+                                                   int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+            passes.append([(meta[i][0], dict(per[i]), meta[i][1]) for i in sorted(per)])
+    return passes
+
+
+def counter_json(dirs, workload: str, xcds: int = 8):
+    """From --pmc passes over `--profile-workload --pw-mode all`: per-launch
+    executed MFMA instructions of the forward and backward kernels with the
+    clock they ran at (profiles/executed_<workload>.json), and the MFMA-busy
+    share of the local-only, global-only and strided-only forward launches
+    (profiles/phases_counters_<workload>.json)."""
+    passes = counter_dispatches(dirs)
+    by_kernel = {}
+    for recs in passes:
+        seen = {}
+        for name, c, ns in recs:
+            i = seen.get(name, 0)
+            seen[name] = i + 1
+            slot = by_kernel.setdefault((name, i), {"ns": []})
+            slot.update(c)
+            slot["ns"].append(ns)
+    def find(prefix, idx=0, suffix=""):
+        for (name, i), c in by_kernel.items():
+            if name.startswith(prefix) and name.endswith(suffix) and i == idx:
+                return c
+        return None
+    fwd = find("fwd2_kernel", 0, ", 3>")
+    dq = find("dq2_kernel")
+    glob_k = find("dkdv2_kernel", 0, ", 128>") or find("dkdv2_kernel", 0, "true, 8, 1, 128>")
+    loc = None
+    for (name, i), c in by_kernel.items():
+        if name.startswith("dkdv2_kernel") and ", false," in name:
+            loc = c
+    mf = {"forward": fwd, "dq": dq, "global_dkdv": glob_k, "local_dkdv": loc}
+    mfma = {k: int(v["SQ_INSTS_MFMA"]) for k, v in mf.items() if v and "SQ_INSTS_MFMA" in v}
+    tot_ns = sum(sum(v["ns"]) / len(v["ns"]) for v in mf.values() if v)
+    clock = sum((v["GRBM_GUI_ACTIVE"] / xcds) for v in mf.values()
+                if v and "GRBM_GUI_ACTIVE" in v) / tot_ns if tot_ns else None
+    executed = {"workload": workload, "mfma_per_launch": mfma,
+                "clock_ghz": round(clock, 3) if clock else None,
+                "how": "SQ_INSTS_MFMA per launch of each kernel of one forward + backward; "
+                       "clock = sum(GRBM_GUI_ACTIVE / 8 XCDs) / sum(duration) over those kernels"}
+    def busy(c):
+        if not c or "SQ_VALU_MFMA_BUSY_CYCLES" not in c or "GRBM_GUI_ACTIVE" not in c:
+            return None
+        return round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] / xcds * CUS * 4), 4)
+    phases = {"local": busy(find("fwd2_kernel", 0, ", 1>")),
+              "global": busy(find("fwd2_kernel", 0, ", 2>")),
+              "strided": busy(find("fwd2_kernel", 1, ", 2>")),
+              "forward": busy(fwd),
+              "how": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x 4 SIMDs) "
+                     "of the local-only, global-only and strided-only (relay-off packing) "
+                     "forward launches of --profile-workload"}
+    return executed, phases
+
+
 def sdpa_backend(q, k, v, torch, F):
     """First fused SDPA backend that runs this shape (flash, then memory
     efficient). The math backend is never used: its batched products on
@@ -629,7 +805,8 @@ def run_crossover(args):
     dev = torch.device("cuda", 0)
     shapes = ((2, 32, 128, torch.bfloat16), (1, 16, 128, torch.float16),
               (1, 8, 64, torch.float16), (1, 12, 64, torch.float16))
-    seqs = (64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384)
+    seqs = (1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 192, 256, 384, 512, 768, 1024, 1536, 2048,
+            3072, 4096, 6144, 8192, 16384)
     for (B, H, D, dtype) in shapes:
         points = []
         backend = None
@@ -659,9 +836,13 @@ def run_crossover(args):
             points.append(res)
             print(json.dumps(res), flush=True)
         summary = {"crossover": True, "B": B, "H": H, "D": D, "dtype": str(dtype).split(".")[-1],
-                   "sdpa_backend": points[0]["sdpa_backend"],
-                   "fwd_crossover_S": first_win(points, "cra_fwd_ms", "sdpa_fwd_ms"),
-                   "train_crossover_S": first_win(points, "cra_train_ms", "sdpa_train_ms")}
+                   "sdpa_backend": points[0]["sdpa_backend"], "swept_from_S": seqs[0]}
+        for mode in ("fwd", "train"):
+            w = first_win(points, f"cra_{mode}_ms", f"sdpa_{mode}_ms")
+            summary[f"{mode}_crossover_S"] = w
+            # a crossover is bracketed when SDPA wins at the swept S just below it
+            summary[f"{mode}_kind"] = ("sqrt(N) op faster at every swept S" if w == seqs[0]
+                                       else "no win in the sweep" if w is None else "bracketed")
         print(json.dumps(summary), flush=True)
 
 
@@ -683,6 +864,16 @@ def main(argv=None):
                     help="copy calibration + hot-path kernels once, for counter passes")
     ap.add_argument("--counter-summary", nargs="+", metavar="DIR",
                     help="print a markdown summary of rocprofv3 --pmc output directories")
+    ap.add_argument("--json-out", metavar="WORKLOAD", default=None,
+                    help="with --counter-summary: also write profiles/executed_WORKLOAD.json and "
+                         "profiles/phases_counters_WORKLOAD.json")
+    ap.add_argument("--pw", default="1,16,131072,128", metavar="B,H,S,D",
+                    help="shape of --profile-workload (fp16)")
+    ap.add_argument("--pw-mode", default="all", choices=("all", "train", "fwd"),
+                    help="what --profile-workload runs")
+    ap.add_argument("--phases", default=None, metavar="S[,S]",
+                    help="per-phase forward figures at B=1 H=16 D=128 fp16 for these S "
+                         "(BASELINE config 3), one JSON line each")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -690,6 +881,12 @@ def main(argv=None):
         return 2
     if args.counter_summary:
         print(counter_summary(args.counter_summary))
+        if args.json_out:
+            ex, ph = counter_json(args.counter_summary, args.json_out)
+            for name, obj in (("executed", ex), ("phases_counters", ph)):
+                with open(os.path.join(ROOT, "profiles", f"{name}_{args.json_out}.json"), "w") as f:
+                    json.dump(obj, f, indent=1)
+                    f.write("\n")
         return 0
     if args.config:
         run_configs(args)
@@ -699,6 +896,8 @@ def main(argv=None):
         run_sdpa_dense(args)
     elif args.profile_workload:
         run_profile_workload(args)
+    elif args.phases:
+        run_phases(args)
     else:
         run_main(args)
     return 0
