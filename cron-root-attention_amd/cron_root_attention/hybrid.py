@@ -5,11 +5,14 @@ The reference's crossover (1536 tokens, hybrid.py:22) was measured on an RTX
 ``bench.py --crossover`` against ROCm's fused (flash) SDPA, causal, for
 forward and forward+backward separately: ``CROSSOVER_GFX950``.  Below a few
 thousand tokens the sqrt(N) op costs its launch floor (about 15 us forward
-and 80-110 us forward+backward through the C++ operator) while SDPA's floor
-is 25 us and 110-130 us and grows with B*H*S^2; on two boxes the sqrt(N) op
-was the faster at every swept S from 64 up, for every BASELINE shape and both
-modes, so every row is 64, the smallest swept S.  The table keeps its shape
-(mode, head dim, B*H) for re-measurement on other hosts.
+and 75-85 us forward+backward through the C++ operator) while SDPA's floor
+is 20-25 us and 82-100 us and grows with B*H*S^2.  Swept from S = 1 to 16384
+for every BASELINE shape in both modes, the sqrt(N) op was the faster at
+every S, so no crossover exists to bracket: every row is 1 (run the sqrt(N)
+op for every length) and ``CROSSOVER_BRACKETED`` says so.  The narrowest
+margin is at S = 1 in training (0.082 against 0.084 ms at B=2 H=32 D=128).
+The table keeps its shape (mode, head dim, B*H) for re-measurement on other
+hosts.
 ``_SDPA_THRESHOLD`` is the forward+backward crossover at D=128 for B*H=16, the
 role of the reference's constant.  Both entry points default to
 ``threshold=None``, which looks the crossover up in the table for the call's
@@ -27,30 +30,49 @@ import torch.nn.functional as F
 from .core import cron_root_attention_v14
 
 # (mode, head_dim, smallest B*H the row applies to) -> smallest swept S from
-# which the sqrt(N) op beats SDPA at every larger swept S, on both boxes.
-# Sweep: S in {64, 128, 256, 384, 512, 768, 1024, 1536, 2048, 3072, 4096,
-# 6144, 8192, 16384}; shapes (B, H, D, dtype) = (1, 16, 128, fp16),
-# (2, 32, 128, bf16), (1, 8, 64, fp16), (1, 12, 64, fp16).
+# which the sqrt(N) op beats SDPA at every larger swept S.
+# Sweep: S in {1, 2, 4, 8, 16, 32, 48, 64, 96, 128, 192, 256, 384, 512, 768,
+# 1024, 1536, 2048, 3072, 4096, 6144, 8192, 16384}; shapes (B, H, D, dtype) =
+# (1, 16, 128, fp16), (2, 32, 128, bf16), (1, 8, 64, fp16), (1, 12, 64, fp16).
+# sqrt(N) op / SDPA ms at S = 1 in each row's comment.
 CROSSOVER_GFX950 = {
-    ("fwd", 128, 1): 64,       # B=1 H=16 fp16: 0.015 vs 0.025 ms at S=64
-    ("fwd", 128, 64): 64,      # B=2 H=32 bf16: 0.020 vs 0.026 ms
-    ("train", 128, 1): 64,     # B=1 H=16 fp16: 0.091 vs 0.118 ms
-    ("train", 128, 64): 64,    # B=2 H=32 bf16: 0.097 vs 0.131 ms
-    ("fwd", 64, 1): 64,        # B=1 H=8 and H=12 fp16: 0.015 vs 0.025 ms
-    ("train", 64, 1): 64,      # B=1 H=8 and H=12 fp16: 0.090 vs 0.116 ms
+    ("fwd", 128, 1): 1,        # B=1 H=16 fp16: 0.016 vs 0.021 ms
+    ("fwd", 128, 64): 1,       # B=2 H=32 bf16: 0.017 vs 0.020 ms
+    ("train", 128, 1): 1,      # B=1 H=16 fp16: 0.081 vs 0.087 ms
+    ("train", 128, 64): 1,     # B=2 H=32 bf16: 0.082 vs 0.084 ms
+    ("fwd", 64, 1): 1,         # B=1 H=8 and H=12 fp16: 0.015-0.016 vs 0.020 ms
+    ("train", 64, 1): 1,       # B=1 H=8 and H=12 fp16: 0.077-0.078 vs 0.082-0.083 ms
 }
+# Whether SDPA won at a swept S below the row's value (a measured, bracketed
+# crossover). False: the sqrt(N) op was faster at every swept S, the row is
+# the sweep's lower edge and no crossover exists in the measured range.
+CROSSOVER_BRACKETED = {key: False for key in CROSSOVER_GFX950}
 _SDPA_THRESHOLD = CROSSOVER_GFX950[("train", 128, 1)]
 
 
-def crossover(head_dim: int, training: bool, batch_heads: int = 1) -> int:
-    """Measured gfx950 crossover for the nearest tabulated head dim and the
-    largest tabulated B*H not above ``batch_heads``."""
+def _row(head_dim: int, training: bool, batch_heads: int):
     mode = "train" if training else "fwd"
     dims = sorted({d for (m, d, _) in CROSSOVER_GFX950 if m == mode})
     d = min(dims, key=lambda x: abs(x - head_dim))
     rows = sorted(bh for (m, dd, bh) in CROSSOVER_GFX950 if m == mode and dd == d)
     bh = max([r for r in rows if r <= max(1, batch_heads)] or rows[:1])
-    return CROSSOVER_GFX950[(mode, d, bh)]
+    return (mode, d, bh)
+
+
+def crossover(head_dim: int, training: bool, batch_heads: int = 1, detail: bool = False):
+    """Measured gfx950 crossover for the nearest tabulated head dim and the
+    largest tabulated B*H not above ``batch_heads``: the S from which the
+    sqrt(N) op runs.  With ``detail=True`` a dict that also says whether the
+    crossover was bracketed by the sweep or the sqrt(N) op was the faster at
+    every swept S (then no SDPA range exists)."""
+    key = _row(head_dim, training, batch_heads)
+    S = CROSSOVER_GFX950[key]
+    if not detail:
+        return S
+    br = CROSSOVER_BRACKETED[key]
+    return {"S": S, "bracketed": br, "row": key,
+            "meaning": ("measured crossover: SDPA is faster below S" if br else
+                        "no crossover: the sqrt(N) op was faster at every swept S (from 1)")}
 
 
 def dispatch_backend(S: int, head_dim: int, training: bool, batch_heads: int = 1,

@@ -114,6 +114,10 @@ def test_crossover_table_lookup():
     assert crossover(112, True, 16) == CROSSOVER_GFX950[("train", 128, 1)]
     assert crossover(32, False, 16) == CROSSOVER_GFX950[("fwd", 64, 1)]
     assert _SDPA_THRESHOLD == CROSSOVER_GFX950[("train", 128, 1)]
+    # the sweep found no crossover: detail says so
+    info = crossover(128, True, 64, detail=True)
+    assert info["S"] == CROSSOVER_GFX950[("train", 128, 64)] and info["bracketed"] is False
+    assert "no crossover" in info["meaning"]
     # more parallel work never raises the crossover
     for mode in ("fwd", "train"):
         for d in (64, 128):

@@ -190,7 +190,9 @@ def test_hybrid_training_mode_uses_training_crossover(monkeypatch):
 
 @pytest.mark.parametrize("S", [48, 4096])
 def test_hybrid_module(S):
-    """CronRootAttentionHybrid (default threshold = the gfx950 table)."""
+    """CronRootAttentionHybrid: the default threshold (the gfx950 table, whose
+    rows say the sqrt(N) op at every length) and explicit thresholds on
+    either side of S, so that both backends run."""
     B, H, D = 1, 8, 64
     E = H * D
     say(f"CronRootAttentionHybrid S={S}")
@@ -206,14 +208,14 @@ def test_hybrid_module(S):
         q, k, v = (_heads(p(x), B, S, H, D) for p in (m.q_proj, m.k_proj, m.v_proj))
         backend = dispatch_backend(S, D, False, B * H)
         assert backend == ("sdpa" if S < crossover(D, False, B * H) else "cron_root")
-        assert backend == ("sdpa" if S == 48 else "cron_root")  # both branches covered
         _check_backend(_heads(box[0], B, S, H, D), q, k, v, backend, F16, [(0, 0), (0, 7)])
-        m2 = cra.CronRootAttentionHybrid(E, H, threshold=S).to(DEV, F16).eval()
-        m2.load_state_dict(m.state_dict())
-        box2, hook2 = _capture(m2.o_proj)
-        m2(x)
-        hook2.remove()
-        _check_backend(_heads(box2[0], B, S, H, D), q, k, v, "cron_root", F16, [(0, 3)])
+        for thr, expect in ((S, "cron_root"), (S + 1, "sdpa")):
+            m2 = cra.CronRootAttentionHybrid(E, H, threshold=thr).to(DEV, F16).eval()
+            m2.load_state_dict(m.state_dict())
+            box2, hook2 = _capture(m2.o_proj)
+            m2(x)
+            hook2.remove()
+            _check_backend(_heads(box2[0], B, S, H, D), q, k, v, expect, F16, [(0, 3)])
 
 
 # ---------------------------------------------------------------- modules
