@@ -351,8 +351,9 @@ def run_main(args):
             "executed_frac": round(flops_ex / (step_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
             # MFMA-busy share every SIMD would need for half the nominal
             # peak, at the clock these kernels sustain (counter summary)
+            # (the step would take f_all / (TARGET_FRAC * peak) at that fraction)
             "mfma_busy_needed_for_half_peak": round(
-                n_mfma * 16 / (TARGET_FRAC * f_all / (PEAK_FP16_TFLOPS * 1e12)
+                n_mfma * 16 / (f_all / (TARGET_FRAC * PEAK_FP16_TFLOPS * 1e12)
                                * ex["clock_ghz"] * 1e9 * CUS * 4), 4),
             "clock_ghz": ex["clock_ghz"], "per_kernel": ex["mfma_per_launch"],
             "source": "profiles/executed_" + workload + ".json"})
