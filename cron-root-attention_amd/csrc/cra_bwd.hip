@@ -746,8 +746,13 @@ void dq2_kernel(BwdArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hq;
-  const int bh = blockIdx.x % nbh;
-  const Doc dc = find_doc(a.docs, (int)(blockIdx.x / nbh));
+  int item = (int)blockIdx.x;
+  if (a.xcd_nt > 0) {
+    item = xcd_item(item, nbh, a.xcd_nt);
+    if (item < 0) return;  // padding block
+  }
+  const int bh = item % nbh;
+  const Doc dc = find_doc(a.docs, item / nbh);
   const int tile = (dc.len + kBM - 1) / kBM - 1 - dc.item;  // heaviest first
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
@@ -1056,8 +1061,13 @@ void dkdv2_kernel(BwdArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, g = lane >> 4;
   const int nbh = a.B * a.Hkv;
-  const int bhk = blockIdx.x % nbh;
-  const int rest = blockIdx.x / nbh;
+  int item = (int)blockIdx.x;
+  if (!GLOB && a.xcd_nt > 0) {
+    item = xcd_item(item, nbh, a.xcd_nt);
+    if (item < 0) return;  // padding block
+  }
+  const int bhk = item % nbh;
+  const int rest = item / nbh;
   const Doc dc = find_doc(a.docs, rest);
   const int chunk = GLOB ? dc.item % a.nchunk : 0;
   const int tile = GLOB ? dc.item / a.nchunk : dc.item;
@@ -1366,8 +1376,16 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   set_items(al.docs, [&](int d) { return (a.docs.len[d] + kLK - 1) / kLK; });
   const int nq = aq.docs.item0[a.docs.n], ng = ag.docs.item0[a.docs.n];
   const int nl = al.docs.item0[a.docs.n];
+  // one document, D = 128 and a head count that is not a multiple of 8: the
+  // dQ and local dK/dV kernels run in the XCD-aware order (as the forward)
+  const bool xq = kTiled && D == 128 && a.docs.n == 1 && (a.B * a.Hq) % 8 != 0;
+  const bool xl = kTiled && D == 128 && a.docs.n == 1 && (a.B * a.Hkv) % 8 != 0;
+  aq.xcd_nt = xq ? nq : 0;
+  al.xcd_nt = xl ? nl : 0;
+  const int gq = xq ? xcd_grid(a.B * a.Hq, nq) : nq * a.B * a.Hq;
+  const int gl = xl ? xcd_grid(a.B * a.Hkv, nl) : nl * a.B * a.Hkv;
   if constexpr (kTiled) {
-    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, kDqQB, kDqBN, kDqWPE>), dim3(nq * a.B * a.Hq),
+    hipLaunchKernelGGL((dq2_kernel<T, D, kDqWaves, kDqQB, kDqBN, kDqWPE>), dim3(gq),
                        dim3(64 * kDqWaves), 0, st, aq);
     hipLaunchKernelGGL((dkdv2_kernel<T, D, true, kDkdvGlobWaves<D>, kDkdvKB, kDkdvGlobBQ>),
                        dim3(ng * a.B * a.Hkv), dim3(64 * kDkdvGlobWaves<D>), 0, st, ag);
@@ -1388,7 +1406,7 @@ hipError_t launch_TD(const BwdArgs& a, hipStream_t st) {
   if (a.dalpha) hipLaunchKernelGGL((dalpha_kernel<T, D>), dim3(a.Hkv), dim3(256), 0, st, a);
   if constexpr (kTiled)
     hipLaunchKernelGGL((dkdv2_kernel<T, D, false, kDkdvLocalWaves, kDkdvLocalKB<D>, kDkdvLocalBQ>),
-                       dim3(nl * a.B * a.Hkv), dim3(64 * kDkdvLocalWaves), 0, st, al);
+                       dim3(gl), dim3(64 * kDkdvLocalWaves), 0, st, al);
   else
     hipLaunchKernelGGL((dkdv_kernel<T, D, NB, false>), dim3(nl * a.B * a.Hkv), dim3(256), 0, st,
                        al);

@@ -655,7 +655,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D == 12
 void fwd2_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) FwdStage<D> stage0;
   __shared__ __attribute__((aligned(1024))) FwdStage<D> stage1;
-  fwd2_item<T, D, NW, PH>(a, (int)blockIdx.x, stage0, stage1);
+  int item = (int)blockIdx.x;
+  if (a.xcd_nt > 0) {
+    item = xcd_item(item, a.B * a.Hq, a.xcd_nt);
+    if (item < 0) return;  // padding block
+  }
+  fwd2_item<T, D, NW, PH>(a, item, stage0, stage1);
 }
 
 // Persistent form (use_persistent; the reference's work-queue kernel,
@@ -732,6 +737,13 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
     constexpr int kBM = 32 * kFwdWaves;
     set_items(b.docs, [&](int d) { return (b.docs.len[d] + kBM - 1) / kBM; });
     const dim3 grid(b.docs.item0[b.docs.n] * b.B * b.Hq), block(64 * kFwdWaves);
+    // one document, D = 128 and a head count that is not a multiple of 8:
+    // XCD-aware order (measured 2.5-5% faster at D = 128; at D = 64, with
+    // 45% less HBM traffic, 0.5% faster to 3.6% slower)
+    const bool xcd = b.docs.n == 1 && (b.B * b.Hq) % 8 != 0 && D == 128;
+    FwdArgs bx = b;
+    bx.xcd_nt = xcd ? b.docs.item0[1] : 0;
+    const dim3 xgrid(xcd ? xcd_grid(b.B * b.Hq, b.docs.item0[1]) : grid.x);
     hipError_t qerr = hipSuccess;
     auto go = [&](auto dc) {
       constexpr int Dc = decltype(dc)::value;
@@ -747,9 +759,9 @@ hipError_t launch_T(int D, const FwdArgs& a, hipStream_t st) {
         return;
       }
       switch (a.phases) {
-        case 1: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 1>), grid, block, 0, st, b); break;
-        case 2: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 2>), grid, block, 0, st, b); break;
-        default: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 3>), grid, block, 0, st, b);
+        case 1: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 1>), xgrid, block, 0, st, bx); break;
+        case 2: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 2>), xgrid, block, 0, st, bx); break;
+        default: hipLaunchKernelGGL((fwd2_kernel<T, Dc, kFwdWaves, 3>), xgrid, block, 0, st, bx);
       }
     };
     switch (D) {

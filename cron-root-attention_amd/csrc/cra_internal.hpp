@@ -36,6 +36,74 @@ __device__ __forceinline__ Doc find_doc(const Docs& t, int item) {
   return Doc{t.off[d], t.len[d], t.W[d], t.rpb[d], t.gofs[d], t.bofs[d], item - t.item0[d]};
 }
 
+// XCD-aware work order for launches of nbh heads x nt tiles (one document)
+// when nbh is not a multiple of 8. The dispatcher sends block i to XCD i % 8;
+// the plain order (item = rank * nbh + head, rank 0 the heaviest tile) then
+// spreads a head's neighbouring tiles over several XCDs, whose L2s do not
+// share the K/V (or Q/dO) rows those tiles overlap on. Here a head's tiles
+// pair up as units {rank p, rank nt - 1 - p} (a heavy and a light tile: every
+// unit costs about the same), units are numbered head by head (u = head * P +
+// p), and XCD x takes a contiguous eighth of them, so it holds about nbh / 8
+// heads with an equal share of the work. Its blocks take its tiles in the
+// plain order's sequence (by rank, then head): heaviest first, as there.
+// xcd_item returns the plain order's item index, or -1 for a padding block.
+struct XcdChunk {
+  int P, Pl;    // units per head; units with a light tile (the middle tile of
+                // an odd nt is its unit's only tile)
+  int q0, r0;   // first unit of this XCD: head q0, p = r0
+  int q1, r1;   // one past its last unit
+};
+
+__host__ __device__ inline XcdChunk xcd_chunk(int x, int nbh, int nt) {
+  const int P = (nt + 1) >> 1, U = nbh * P;
+  const int base = U >> 3, extra = U & 7;
+  const int u0 = x * base + (x < extra ? x : extra);
+  const int u1 = u0 + base + (x < extra ? 1 : 0);
+  return XcdChunk{P, nt >> 1, u0 / P, u0 % P, u1 / P, u1 % P};
+}
+
+// units of the chunk with p in [a, b)
+__host__ __device__ inline int xcd_units(const XcdChunk& c, int a, int b) {
+  if (a >= b) return 0;
+  const int e1 = c.r1 < a ? a : c.r1 > b ? b : c.r1;
+  const int e0 = c.r0 < a ? a : c.r0 > b ? b : c.r0;
+  return (c.q1 - c.q0) * (b - a) + e1 - e0;
+}
+
+// tiles of the chunk with rank < r
+__host__ __device__ inline int xcd_before(const XcdChunk& c, int nt, int r) {
+  const int heavy = xcd_units(c, 0, r < c.P ? r : c.P);
+  const int a = nt - r > 0 ? nt - r : 0;
+  return heavy + xcd_units(c, a < c.Pl ? a : c.Pl, c.Pl);
+}
+
+__host__ __device__ inline int xcd_grid(int nbh, int nt) {
+  int most = 0;
+  for (int x = 0; x < 8; ++x) {
+    const XcdChunk c = xcd_chunk(x, nbh, nt);
+    const int n = xcd_before(c, nt, nt);
+    most = n > most ? n : most;
+  }
+  return 8 * most;
+}
+
+__host__ __device__ inline int xcd_item(int block, int nbh, int nt) {
+  const XcdChunk c = xcd_chunk(block & 7, nbh, nt);
+  const int k = block >> 3;
+  if (k >= xcd_before(c, nt, nt)) return -1;  // padding block
+  // the rank r with xcd_before(r) <= k < xcd_before(r + 1)
+  int lo = 0, hi = nt - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (xcd_before(c, nt, mid) <= k) lo = mid; else hi = mid - 1;
+  }
+  const int r = lo;
+  const int p = r < c.P ? r : nt - 1 - r;
+  // heads whose unit p lies in the chunk form a run from head q0 (q0 + 1
+  // when unit (q0, p) precedes the chunk); take the j-th
+  return r * nbh + c.q0 + (p < c.r0 ? 1 : 0) + (k - xcd_before(c, nt, r));
+}
+
 struct GlobalArgs {
   const void* k;
   const void* v;
@@ -65,6 +133,7 @@ struct FwdArgs {
   float scale;
   int phases;  // bit 0: local window, bit 1: global rows
   int* work_counter;  // persistent launch: zeroed item counter, else null
+  int xcd_nt;  // > 0: XCD-aware order (xcd_item) over this many tiles per head
   Docs docs;   // items: query tiles (set by the launcher for its tile size)
 };
 
@@ -96,6 +165,7 @@ struct BwdArgs {
   int nchunk;      // query chunks per document of the global-row kernel
   int group;       // 0: first launch of a call (fp32: computes Delta; writes dalpha);
                    // later document groups of the call add to dalpha
+  int xcd_nt;      // > 0: XCD-aware order (xcd_item) over this many tiles per head
   Docs docs;       // items: set by the launcher per kernel
 };
 

@@ -77,6 +77,9 @@ FWD_CASES = [
     (BF16, 1, 2, 2, 1000, 64, 2), (F32, 1, 2, 2, 4096, 64, 2), (F32, 1, 2, 2, 777, 128, 2),
     (F32, 1, 2, 2, 3001, 32, 2), (F16, 1, 2, 2, 16, 16, 2), (F16, 1, 2, 2, 2100, 80, 2),
     (BF16, 1, 2, 1, 3333, 96, 2),
+    # 10 heads at D = 128 (not a multiple of 8: the XCD-aware block order)
+    # over an odd number of query tiles
+    (F16, 2, 5, 5, 1300, 128, 2),
 ]
 
 
@@ -174,6 +177,9 @@ BWD_CASES = [
     # top-1 and top-3 in the 2-byte kernels; 8 query heads per kv head
     (F16, 1, 2, 2, 1, 64, 2), (F16, 1, 2, 2, 33, 128, 2), (F16, 1, 2, 2, 4500, 128, 1),
     (BF16, 1, 4, 2, 3500, 128, 3), (F16, 1, 8, 1, 2200, 128, 2),
+    # 10 heads at D = 128: the XCD-aware block order of the dQ and local
+    # dK/dV kernels over odd tile counts
+    (F16, 2, 5, 5, 1300, 128, 2),
 ]
 
 
