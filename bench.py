@@ -205,6 +205,15 @@ def cpu_baseline(B, H, S, D, budget_s: float, threads: int):
     return out
 
 
+def mfma_busy_needed(n_mfma: float, flops: float, clock_ghz: float, frac: float) -> float:
+    """Share of cycles every SIMD's matrix core must be busy (16 cycles per
+    executed v_mfma_f32_16x16x32) for `flops` of algorithmic work to run at
+    `frac` of the nominal fp16 peak, at the clock `clock_ghz`: the step then
+    takes flops / (frac * peak) seconds."""
+    seconds = flops / (frac * PEAK_FP16_TFLOPS * 1e12)
+    return n_mfma * 16 / (seconds * clock_ghz * 1e9 * CUS * 4)
+
+
 def executed_for(workload: str):
     """Executed MFMA instructions per kernel launch (SQ_INSTS_MFMA) and the
     sustained clock, from the committed counter summary of this workload
@@ -351,10 +360,8 @@ def run_main(args):
             "executed_frac": round(flops_ex / (step_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
             # MFMA-busy share every SIMD would need for half the nominal
             # peak, at the clock these kernels sustain (counter summary)
-            # (the step would take f_all / (TARGET_FRAC * peak) at that fraction)
             "mfma_busy_needed_for_half_peak": round(
-                n_mfma * 16 / (f_all / (TARGET_FRAC * PEAK_FP16_TFLOPS * 1e12)
-                               * ex["clock_ghz"] * 1e9 * CUS * 4), 4),
+                mfma_busy_needed(n_mfma, f_all, ex["clock_ghz"], TARGET_FRAC), 4),
             "clock_ghz": ex["clock_ghz"], "per_kernel": ex["mfma_per_launch"],
             "source": "profiles/executed_" + workload + ".json"})
 

@@ -104,6 +104,29 @@ def test_counter_summary_known_figures(tmp_path):
     assert "Calibration" in out and "524288 KiB" in out
 
 
+def test_mfma_busy_needed():
+    # no executed overhead (one MFMA per 16384 algorithmic flops): the busy
+    # share needed equals the target fraction times nominal peak over the
+    # matrix cores' rate at that clock (256 CUs x 4 SIMDs x 1024 flop/cycle)
+    flops = 3384.65e9
+    n = flops / bench.MFMA_FLOPS
+    rate = bench.CUS * 4 * bench.MFMA_FLOPS / 16  # flop per cycle
+    for clock in (1.8, 2.4):
+        want = 0.5 * bench.PEAK_FP16_TFLOPS * 1e12 / (rate * clock * 1e9)
+        assert abs(bench.mfma_busy_needed(n, flops, clock, 0.5) - want) < 1e-12
+    # twice the executed work needs twice the busy share; half the target, half
+    assert abs(bench.mfma_busy_needed(2 * n, flops, 2.4, 0.5)
+               - 2 * bench.mfma_busy_needed(n, flops, 2.4, 0.5)) < 1e-12
+    assert abs(bench.mfma_busy_needed(n, flops, 2.4, 0.25)
+               - 0.5 * bench.mfma_busy_needed(n, flops, 2.4, 0.5)) < 1e-12
+    # the committed north-star counters: about 0.91 at their sustained clock
+    ex = bench.executed_for("H16_D128_S131072_fp16")
+    if ex:
+        need = bench.mfma_busy_needed(sum(ex["mfma_per_launch"].values()), flops,
+                                      ex["clock_ghz"], 0.5)
+        assert 0.8 < need < 1.0, need
+
+
 def test_more_than_one_gpu_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120, cwd=ROOT)
